@@ -1,0 +1,247 @@
+/* sage_hip.h -- C ABI of the MI355X (gfx950) SageAttention2 forward path.
+ *
+ * This is the drop-in boundary for the reference's `spl_nn::sage` Rust API
+ * (sezer-muhammed/sota-papers-lab, platform/spl-nn/src/sage/mod.rs) and the
+ * cudarc backend under it (platform/spl-gpu/src/lib.rs). Each declaration
+ * names the reference item it replaces. Plain pointers, sizes and PODs only;
+ * device pointers are HIP device addresses, the stream is a hipStream_t.
+ *
+ * Semantics kept from the reference:
+ *   - every call enqueues on the context's stream and returns without
+ *     synchronising (mod.rs:509-510); prepare/attend neither allocate nor
+ *     synchronise, so they can be captured in a hipGraph (the workspace is
+ *     allocated once per shape by sage_workspace, mod.rs:649-670);
+ *   - every invalid input is reported before any launch, with the reference's
+ *     error text, through the return status and sage_last_error()
+ *     (mod.rs:251-259,405-440,587-589,681-709,841-852);
+ *   - the caller owns Q/K/V/out device memory (borrowed for the call); the
+ *     library owns the workspace and frees it in sage_workspace_destroy.
+ *
+ * Extensions with no reference counterpart: fp16 inputs
+ * and output (dtype fields), causal masking (sage_options.causal) and
+ * grouped-query heads (sage_shape.kv_heads).
+ */
+#ifndef SAGE_HIP_H
+#define SAGE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Query rows per INT8 Q scale, queries per prologue tile, keys per K/V block
+ * (mod.rs:70-75, sage_common.cu:33-35) and the E4M3 range V is scaled to
+ * (mod.rs:76-77, :183-185). */
+#define SAGE_QGROUP 16
+#define SAGE_QTILE 128
+#define SAGE_KBLOCK 64
+#define SAGE_FP8_MAX 448.0f
+#define SAGE_PV16_V_RANGE 2.25f
+
+typedef enum sage_status {
+    SAGE_OK = 0,
+    SAGE_ERR_INVALID = 1,     /* bad argument: the reference's `bail!` */
+    SAGE_ERR_UNSUPPORTED = 2, /* a reference feature this build does not implement */
+    SAGE_ERR_DEVICE = 3,      /* HIP runtime failure (mod.rs:106-114 `.cuda(what)`) */
+    SAGE_ERR_STATE = 4        /* e.g. attend before prepare (mod.rs:841-843) */
+} sage_status;
+
+/* Element type of a 16-bit tensor. The reference reads and writes bf16 only
+ * (sage_common.cu:66-80); fp16 is an extension. */
+typedef enum sage_dtype { SAGE_BF16 = 0, SAGE_F16 = 1 } sage_dtype;
+
+/* PvAccum (mod.rs:170-181). Only F32 is implemented; F16 returns
+ * SAGE_ERR_UNSUPPORTED. */
+typedef enum sage_pv_accum { SAGE_PV_F32 = 0, SAGE_PV_F16 = 1 } sage_pv_accum;
+
+/* Tile (mod.rs:116-168), re-read for CDNA4: `warps` = wave64s per workgroup,
+ * `m_tiles` = 32-query MFMA column tiles per wave, `stages` = K/V LDS
+ * buffers. Rows per workgroup = 32 * m_tiles * warps. */
+typedef struct sage_tile {
+    uint32_t warps;
+    uint32_t m_tiles;
+    uint32_t stages;
+} sage_tile;
+
+/* Config (mod.rs:187-201). */
+typedef struct sage_config {
+    sage_tile tile;
+    int32_t pv_accum; /* sage_pv_accum */
+} sage_config;
+
+/* Shape (mod.rs:262-268) plus kv_heads (0 = heads; extension: grouped-query
+ * attention, heads must be a multiple of kv_heads). */
+typedef struct sage_shape {
+    uint64_t batch;
+    uint64_t heads;
+    uint64_t tokens;
+    uint64_t kv_heads;
+} sage_shape;
+
+/* FrameLayout (mod.rs:270-300). */
+typedef struct sage_frame_layout {
+    uint64_t frames;
+    uint64_t special;
+    uint64_t grid_h;
+    uint64_t grid_w;
+    uint64_t dense_frames;
+} sage_frame_layout;
+
+/* KvMerge (mod.rs:302-311): stride 1 = Dense, 2 or 4 = Pool{stride, layout}.
+ * Plans are computed for every variant; prepare/attend of a pooled plan
+ * return SAGE_ERR_UNSUPPORTED in this build. */
+typedef struct sage_kv_merge {
+    uint32_t stride;
+    sage_frame_layout layout;
+} sage_kv_merge;
+
+/* Plan (mod.rs:391-454). */
+typedef struct sage_plan {
+    sage_shape shape;
+    sage_kv_merge merge;
+    uint64_t tq_pad; /* tokens rounded up to SAGE_QTILE */
+    uint64_t tk;     /* keys after merging */
+    uint64_t tk_pad; /* tk rounded up to SAGE_KBLOCK */
+} sage_plan;
+
+/* Strides (mod.rs:203-260): element strides of [batch][token][head][dim]
+ * with contiguous channels; each a multiple of 8 elements. */
+typedef struct sage_strides {
+    uint64_t batch;
+    uint64_t token;
+    uint64_t head;
+} sage_strides;
+
+/* Tensor / TensorMut (mod.rs:497-507): a device buffer of `len` elements. */
+typedef struct sage_tensor {
+    const void* data;
+    uint64_t len;
+    sage_strides strides;
+    int32_t dtype; /* sage_dtype */
+} sage_tensor;
+
+typedef struct sage_tensor_mut {
+    void* data;
+    uint64_t len;
+    sage_strides strides;
+    int32_t dtype; /* sage_dtype */
+} sage_tensor_mut;
+
+/* Options (mod.rs:313-335). has_softmax_scale = 0 means the default
+ * 1/sqrt(head_dim). qk_norm_params != NULL asks for the fused QK LayerNorm
+ * (mod.rs:337-344), which returns SAGE_ERR_UNSUPPORTED in this build.
+ * causal is an extension (keys j > i are masked). */
+typedef struct sage_options {
+    float softmax_scale;
+    int32_t has_softmax_scale;
+    int32_t smooth_k;
+    int32_t smooth_v;
+    const float* qk_norm_params;
+    uint64_t qk_norm_len;
+    float qk_norm_eps;
+    int32_t causal;
+} sage_options;
+
+/* Device addresses of a workspace's buffers (the pub fields of Workspace,
+ * mod.rs:456-477), with their element counts. Layouts (b batch, h Q head,
+ * g KV head):
+ *   q8      i8  [b][h][tq_pad][D]          q_scale f32 [b][h][tq_pad/16]
+ *   k8      i8  [b][g][tk_pad][D]          k_scale f32 [b][g][tk_pad/64]
+ *   v8      u8  [b][g][tk_pad/64][D][64]   E4M3, key k of a block at byte
+ *                                          sage_v8_position(k) of its row
+ *   stats   f32 [b][g][4][D]               K mean, V mean, V scale, 1/V scale
+ *   kbias   f32 [tk_pad]                   KV-merge bias (unused when dense) */
+typedef struct sage_ws_buffers {
+    int8_t* q8;
+    float* q_scale;
+    int8_t* k8;
+    float* k_scale;
+    uint8_t* v8;
+    float* stats;
+    float* kbias;
+    uint64_t q8_len, q_scale_len, k8_len, k_scale_len, v8_len, stats_len, kbias_len;
+} sage_ws_buffers;
+
+typedef struct sage_attention sage_attention; /* SageAttention (mod.rs:509-520) */
+typedef struct sage_workspace sage_workspace; /* Workspace (mod.rs:456-495) */
+
+/* Text of the last error on this thread ("" when none). The reference's
+ * anyhow messages, e.g. "sage workspace has not been prepared". */
+const char* sage_last_error(void);
+
+/* Plan::new (mod.rs:405-440). Host only; no GPU needed. */
+sage_status sage_plan_new(const sage_shape* shape, const sage_kv_merge* merge, sage_plan* out);
+
+/* flops (mod.rs:905-910): 4 * B * H * tokens * tk * D. With causal = 1, the
+ * pairs j <= i only: 2 * B * H * D * tokens * (tokens + 1) (extension). */
+double sage_flops(const sage_plan* plan, uint64_t head_dim, int32_t causal);
+
+/* Strides::check (mod.rs:251-259); `what` names the tensor in the message. */
+sage_status sage_strides_check(const sage_strides* s, const char* what);
+
+/* Strides::extent (mod.rs:244-249) for `heads` heads. */
+uint64_t sage_strides_extent(const sage_strides* s, uint64_t batch, uint64_t tokens, uint64_t heads,
+                             uint64_t head_dim);
+
+/* Tile::validate (mod.rs:158-167) for this build's tile menu. */
+sage_status sage_tile_validate(const sage_tile* t);
+
+/* Config::for_head_dim (mod.rs:194-200). */
+sage_config sage_config_for_head_dim(uint64_t head_dim);
+
+/* check_device (mod.rs:552-566): fails unless device `ordinal` is gfx950. */
+sage_status sage_check_device(int ordinal);
+
+/* SageAttention::new / with_config (mod.rs:571-626) on `stream` (a
+ * hipStream_t; NULL = the null stream) of the current device.
+ * config == NULL means Config::for_head_dim. */
+sage_status sage_new(void* stream, uint64_t head_dim, const sage_config* config, sage_attention** out);
+void sage_destroy(sage_attention* s);
+uint64_t sage_head_dim(const sage_attention* s);             /* mod.rs:628-630 */
+sage_config sage_get_config(const sage_attention* s);        /* mod.rs:632-634 */
+void* sage_stream(const sage_attention* s);                  /* mod.rs:636-638 */
+
+/* attn_resources (mod.rs:640-646): VGPRs per lane and scratch (spill) bytes
+ * of the attention kernel, plus its static LDS bytes. */
+sage_status sage_attn_resources(const sage_attention* s, int32_t* regs, int32_t* spill, int32_t* lds);
+
+/* SageAttention::workspace (mod.rs:648-670): allocates (and zero-fills) the
+ * buffers for `shape` and `merge`. */
+sage_status sage_workspace_new(const sage_attention* s, const sage_shape* shape, const sage_kv_merge* merge,
+                           sage_workspace** out);
+void sage_workspace_destroy(sage_workspace* ws);
+uint64_t sage_workspace_bytes(const sage_workspace* ws);                 /* mod.rs:484-494 */
+sage_status sage_workspace_plan(const sage_workspace* ws, sage_plan* out); /* mod.rs:480-482 */
+sage_status sage_workspace_buffers(const sage_workspace* ws, sage_ws_buffers* out);
+
+/* SageAttention::prepare (mod.rs:672-836): K smoothing statistics, INT8 Q
+ * (per 16 rows), INT8 K (per 64 keys), FP8 V (per channel) into `ws`. */
+sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,
+                         const sage_tensor* v, const sage_options* opts);
+
+/* SageAttention::attend (mod.rs:838-886): INT8 QK^T, online exp2 softmax,
+ * FP8 P.V; writes [batch][token][head][dim] into `out`. */
+sage_status sage_attend(const sage_attention* s, const sage_workspace* ws, const sage_tensor_mut* out);
+
+/* SageAttention::forward (mod.rs:888-900): prepare then attend. */
+sage_status sage_forward(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,
+                         const sage_tensor* v, const sage_tensor_mut* out, const sage_options* opts);
+
+/* Byte position of key k (0..63) of a 64-key block inside each channel row
+ * of the v8 layout (the CDNA4 counterpart of sg_vpos, sage_common.cu:151-155):
+ * the order in which the QK^T accumulator of the 32x32 MFMA hands keys to the
+ * FP8 MFMA's operand. Host only. */
+int32_t sage_v8_position(int32_t k);
+
+/* MFMA peak probes (the analogue of sage_peak.cu:10-94 and the tests.rs:757-794
+ * driver): which = 0 INT8 32x32x32 (i32 acc), 1 FP8 E4M3 32x32x64 (f32 acc),
+ * 2 BF16 32x32x16 (f32 acc). Runs on the context's stream, synchronises, and
+ * writes the measured dense TOPS. */
+sage_status sage_peak(const sage_attention* s, int32_t which, int32_t iters, double* tops);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

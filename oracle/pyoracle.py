@@ -1,0 +1,301 @@
+"""numpy front end of the C oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg,
+as the checker. The product (spl_sage / libsage_hip.so) never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+import subprocess
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liboracle.so"
+
+BF16, F16 = 0, 1
+QGROUP, QTILE, KBLOCK = 16, 128, 64
+LOG2E_F32 = np.float32(1.4426950408889634)
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB
+
+
+class _Problem(C.Structure):
+    _fields_ = [
+        ("batch", C.c_int), ("heads", C.c_int), ("kv_heads", C.c_int), ("tokens", C.c_int), ("head_dim", C.c_int),
+        ("dtype", C.c_int),
+        ("q_sb", C.c_longlong), ("q_st", C.c_longlong), ("q_sh", C.c_longlong),
+        ("k_sb", C.c_longlong), ("k_st", C.c_longlong), ("k_sh", C.c_longlong),
+        ("v_sb", C.c_longlong), ("v_st", C.c_longlong), ("v_sh", C.c_longlong),
+        ("q_mul", C.c_float), ("smooth_k", C.c_int), ("smooth_v", C.c_int), ("v_range", C.c_float),
+    ]
+
+
+class _GenSpec(C.Structure):
+    _fields_ = [
+        ("batch", C.c_int), ("heads", C.c_int), ("kv_heads", C.c_int), ("tokens", C.c_int), ("head_dim", C.c_int),
+        ("dtype", C.c_int), ("k_off_std", C.c_float), ("outlier_channels", C.c_int), ("outlier_scale", C.c_float),
+        ("token_frac", C.c_float), ("token_scale", C.c_float), ("seed", C.c_uint64),
+    ]
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        l = C.CDLL(os.fspath(LIB))
+        vp = C.c_void_p
+        l.oracle_bf16_to_f32.restype = C.c_float
+        l.oracle_bf16_to_f32.argtypes = [C.c_uint16]
+        l.oracle_f32_to_bf16.restype = C.c_uint16
+        l.oracle_f32_to_bf16.argtypes = [C.c_float]
+        l.oracle_f16_to_f32.restype = C.c_float
+        l.oracle_f16_to_f32.argtypes = [C.c_uint16]
+        l.oracle_f32_to_f16.restype = C.c_uint16
+        l.oracle_f32_to_f16.argtypes = [C.c_float]
+        l.oracle_e4m3_to_f32.restype = C.c_float
+        l.oracle_e4m3_to_f32.argtypes = [C.c_uint8]
+        l.oracle_f32_to_e4m3.restype = C.c_uint8
+        l.oracle_f32_to_e4m3.argtypes = [C.c_float]
+        l.oracle_s8.restype = C.c_int
+        l.oracle_s8.argtypes = [C.c_float]
+        l.oracle_vpos_ref.restype = C.c_int
+        l.oracle_vpos_ref.argtypes = [C.c_int]
+        for n in ("oracle_decode16", "oracle_encode16"):
+            getattr(l, n).argtypes = [vp, vp, C.c_size_t, C.c_int]
+        l.oracle_e4m3_encode.argtypes = [vp, vp, C.c_size_t]
+        l.oracle_e4m3_decode.argtypes = [vp, vp, C.c_size_t]
+        l.oracle_rng_next.restype = C.c_uint64
+        l.oracle_rng_next.argtypes = [C.POINTER(C.c_uint64)]
+        l.oracle_rng_uniform.restype = C.c_double
+        l.oracle_rng_uniform.argtypes = [C.POINTER(C.c_uint64)]
+        l.oracle_rng_normal.restype = C.c_float
+        l.oracle_rng_normal.argtypes = [C.POINTER(C.c_uint64)]
+        l.oracle_generate.argtypes = [C.POINTER(_GenSpec), vp, vp, vp]
+        l.oracle_reference_synthetic.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_uint64, vp, vp, vp]
+        l.oracle_prologue.restype = C.c_int
+        l.oracle_prologue.argtypes = [C.POINTER(_Problem), vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int]
+        l.oracle_attention_f64.argtypes = [C.POINTER(_Problem), C.c_int, C.c_float, vp, vp, vp, vp, C.c_int, vp, C.c_int]
+        l.oracle_sage_emulate.argtypes = [C.POINTER(_Problem), C.c_int, vp, vp, vp, vp, vp, vp, vp, C.c_int, vp, vp,
+                                          C.c_int, C.c_int]
+        l.oracle_errors.argtypes = [vp, vp, C.c_size_t, vp]
+        _lib = l
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ------------------------------------------------------------------ codecs
+
+def decode16(x: np.ndarray, dtype: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    out = np.empty(x.shape, np.float32)
+    lib().oracle_decode16(_p(x), _p(out), x.size, dtype)
+    return out
+
+
+def encode16(x: np.ndarray, dtype: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().oracle_encode16(_p(x), _p(out), x.size, dtype)
+    return out
+
+
+def e4m3_encode(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, np.uint8)
+    lib().oracle_e4m3_encode(_p(x), _p(out), x.size)
+    return out
+
+
+def e4m3_decode(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.uint8)
+    out = np.empty(x.shape, np.float32)
+    lib().oracle_e4m3_decode(_p(x), _p(out), x.size)
+    return out
+
+
+class Rng:
+    """splitmix64 (reference.rs:227-254)."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(seed)
+
+    def next_u64(self) -> int:
+        return lib().oracle_rng_next(C.byref(self.state))
+
+    def uniform(self) -> float:
+        return lib().oracle_rng_uniform(C.byref(self.state))
+
+    def normal(self) -> float:
+        return lib().oracle_rng_normal(C.byref(self.state))
+
+
+# ------------------------------------------------------------------ problems
+
+@dataclass
+class Problem:
+    """One attention problem, inputs in [b][t][h][d] layout (bthd) unless strides given."""
+
+    batch: int
+    heads: int
+    tokens: int
+    head_dim: int
+    kv_heads: int = 0
+    dtype: int = BF16
+    causal: bool = False
+    smooth_k: bool = True
+    smooth_v: bool = True
+    softmax_scale: float | None = None
+    strides: dict = field(default_factory=dict)  # optional {"q": (sb, st, sh), "k": ..., "v": ...}
+
+    @property
+    def hk(self) -> int:
+        return self.kv_heads or self.heads
+
+    @property
+    def tq_pad(self) -> int:
+        return -(-self.tokens // QTILE) * QTILE
+
+    @property
+    def tk_pad(self) -> int:
+        return -(-self.tokens // KBLOCK) * KBLOCK
+
+    def scale(self) -> np.float32:
+        if self.softmax_scale is not None:
+            return np.float32(self.softmax_scale)
+        return np.float32(1.0) / np.sqrt(np.float32(self.head_dim))
+
+    def q_mul(self) -> np.float32:
+        return np.float32(self.scale() * LOG2E_F32)
+
+    def _c(self) -> _Problem:
+        d, t = self.head_dim, self.tokens
+        def dflt(h):
+            return (t * h * d, h * d, d)
+        q = self.strides.get("q", dflt(self.heads))
+        k = self.strides.get("k", dflt(self.hk))
+        v = self.strides.get("v", dflt(self.hk))
+        return _Problem(self.batch, self.heads, self.hk, t, d, self.dtype, *q, *k, *v, float(self.q_mul()),
+                        int(self.smooth_k), int(self.smooth_v), 448.0)
+
+
+@dataclass
+class GenSpec:
+    k_off_std: float = 2.0
+    outlier_channels: int = 0
+    outlier_scale: float = 1.0
+    token_frac: float = 0.0
+    token_scale: float = 1.0
+    seed: int = 1
+
+
+def generate(p: Problem, g: GenSpec):
+    """Seeded synthetic Q, K, V (uint16 codes of p.dtype), shapes [B,T,H,D] / [B,T,HKV,D]."""
+    q = np.empty((p.batch, p.tokens, p.heads, p.head_dim), np.uint16)
+    k = np.empty((p.batch, p.tokens, p.hk, p.head_dim), np.uint16)
+    v = np.empty_like(k)
+    s = _GenSpec(p.batch, p.heads, p.hk, p.tokens, p.head_dim, p.dtype, g.k_off_std, g.outlier_channels,
+                 g.outlier_scale, g.token_frac, g.token_scale, g.seed)
+    lib().oracle_generate(C.byref(s), _p(q), _p(k), _p(v))
+    return q, k, v
+
+
+def reference_synthetic(p: Problem, seed: int):
+    """The reference tests' clustered bf16 activations (tests.rs:300-329), [B,T,H,D]."""
+    assert p.dtype == BF16 and p.hk == p.heads
+    shape = (p.batch, p.tokens, p.heads, p.head_dim)
+    q, k, v = (np.empty(shape, np.uint16) for _ in range(3))
+    lib().oracle_reference_synthetic(p.batch, p.tokens, p.heads, p.head_dim, seed, _p(q), _p(k), _p(v))
+    return q, k, v
+
+
+def prologue(p: Problem, q: np.ndarray, k: np.ndarray, v: np.ndarray, threads: int = 0) -> dict:
+    """Bit-exact restatement of the reference prologue; logical layouts."""
+    B, H, HK, D = p.batch, p.heads, p.hk, p.head_dim
+    out = {
+        "q8": np.zeros((B, H, p.tq_pad, D), np.int8),
+        "q_scale": np.zeros((B, H, p.tq_pad // QGROUP), np.float32),
+        "k8": np.zeros((B, HK, p.tk_pad, D), np.int8),
+        "k_scale": np.zeros((B, HK, p.tk_pad // KBLOCK), np.float32),
+        "v8": np.zeros((B, HK, p.tk_pad, D), np.uint8),
+        "stats": np.zeros((B, HK, 4, D), np.float32),
+    }
+    q, k, v = (np.ascontiguousarray(a, dtype=np.uint16) for a in (q, k, v))
+    r = lib().oracle_prologue(C.byref(p._c()), _p(q), _p(k), _p(v), _p(out["q8"]), _p(out["q_scale"]),
+                              _p(out["k8"]), _p(out["k_scale"]), _p(out["v8"]), _p(out["stats"]), threads)
+    if r != 0:
+        raise ValueError("oracle prologue: unsupported head dim")
+    return out
+
+
+def _rows(rows, n):
+    if rows is None:
+        return None, n
+    r = np.ascontiguousarray(rows, dtype=np.int32)
+    assert r.min() >= 0 and r.max() < n
+    return r, len(r)
+
+
+def attention_f64(p: Problem, q, k, v, rows=None, threads: int = 0) -> np.ndarray:
+    """f64 softmax attention (reference.rs:148-184), [B, H, R, D] float32."""
+    r, R = _rows(rows, p.tokens)
+    out = np.empty((p.batch, p.heads, R, p.head_dim), np.float32)
+    q, k, v = (np.ascontiguousarray(a, dtype=np.uint16) for a in (q, k, v))
+    lib().oracle_attention_f64(C.byref(p._c()), int(p.causal), float(p.scale()), _p(q), _p(k), _p(v),
+                               None if r is None else _p(r), R, _p(out), threads)
+    return out
+
+
+def sage_emulate(p: Problem, pro: dict, rows=None, out_dtype: int = BF16, threads: int = 0):
+    """The reference's quantised attention arithmetic on `pro`; returns
+    (float32 [B,H,R,D] before 16-bit rounding, uint16 codes of out_dtype)."""
+    r, R = _rows(rows, p.tokens)
+    out = np.empty((p.batch, p.heads, R, p.head_dim), np.float32)
+    o16 = np.empty(out.shape, np.uint16)
+    lib().oracle_sage_emulate(C.byref(p._c()), int(p.causal), _p(pro["q8"]), _p(pro["q_scale"]), _p(pro["k8"]),
+                              _p(pro["k_scale"]), _p(pro["v8"]), _p(pro["stats"]), None if r is None else _p(r), R,
+                              _p(out), _p(o16), out_dtype, threads)
+    return out, o16
+
+
+def errors(ours: np.ndarray, ref: np.ndarray) -> dict:
+    """reference.rs:186-225: cos, rel_l1, rel_l2, max_abs, ref_max."""
+    a = np.ascontiguousarray(ours, dtype=np.float32).ravel()
+    b = np.ascontiguousarray(ref, dtype=np.float32).ravel()
+    assert a.size == b.size
+    o = np.zeros(5, np.float64)
+    lib().oracle_errors(_p(a), _p(b), a.size, _p(o))
+    return dict(cos=o[0], rel_l1=o[1], rel_l2=o[2], max_abs=o[3], ref_max=o[4])
+
+
+# The BASELINE configs (BASELINE.json "configs"), as (Problem, GenSpec).
+def config(n: int, seed: int = 1):
+    if n == 1:
+        return Problem(1, 2, 256, 64, dtype=F16), GenSpec(k_off_std=2.0, seed=seed)
+    if n == 2:
+        return Problem(2, 32, 4096, 128, dtype=BF16), GenSpec(k_off_std=2.0, seed=seed)
+    if n == 3:
+        return (Problem(1, 32, 16384, 128, dtype=F16, causal=True),
+                GenSpec(k_off_std=2.0, outlier_channels=4, outlier_scale=20.0, seed=seed))
+    if n == 4:
+        return (Problem(1, 32, 8192, 128, kv_heads=8, dtype=BF16, causal=True, softmax_scale=1 / math.sqrt(128)),
+                GenSpec(k_off_std=2.0, seed=seed))
+    if n == 5:
+        return (Problem(1, 48, 17776, 64, dtype=F16),
+                GenSpec(k_off_std=3.0, token_frac=0.02, token_scale=10.0, seed=seed))
+    raise ValueError(n)

@@ -1,0 +1,132 @@
+/* CPU oracle for the SageAttention2 forward path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * This library is the checker the parity tests, the smoke test and the CPU
+ * baseline leg of bench.py compare the HIP path against. The product path
+ * (libsage_hip.so) never links, loads or calls it.
+ *
+ * It restates, in plain C, the arithmetic of the reference
+ * (sezer-muhammed/sota-papers-lab, platform/spl-nn):
+ *   - codecs            src/sage/reference.rs:8-70, cuda/sage_common.cu:76-99
+ *   - splitmix64 RNG    src/sage/reference.rs:228-254
+ *   - prologue          cuda/sage_quant.cu:59-206 (sg_prep, sg_finalize) and
+ *                       :238-326 (sg_quant_kv), fp32 operation order kept
+ *   - f64 attention     src/sage/reference.rs:148-184 (+ causal, GQA)
+ *   - sage emulator     cuda/sage_attn.cu:262-344,402-421 semantics
+ *   - error metrics     src/sage/reference.rs:202-225
+ *
+ * Pinning status of each function is listed in oracle/README.md (the header
+ * of each function in sage_oracle.c says what pins it).
+ */
+#ifndef SAGE_ORACLE_H
+#define SAGE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORACLE_BF16 = 0, ORACLE_F16 = 1 };
+
+/* Constants of the reference (cuda/sage_common.cu:33-35, src/sage/mod.rs:70-77). */
+#define ORACLE_QGROUP 16
+#define ORACLE_QTILE 128
+#define ORACLE_KBLOCK 64
+#define ORACLE_FP8_MAX 448.0f
+
+/* One attention problem. Q has `heads` heads, K and V `kv_heads` (== heads
+ * unless grouped-query). Element strides of the 16-bit inputs, channels
+ * contiguous. */
+typedef struct {
+    int batch, heads, kv_heads, tokens, head_dim;
+    int dtype; /* ORACLE_BF16 or ORACLE_F16 */
+    long long q_sb, q_st, q_sh;
+    long long k_sb, k_st, k_sh;
+    long long v_sb, v_st, v_sh;
+    float q_mul;   /* softmax scale * log2(e), computed in f32 */
+    int smooth_k;  /* subtract the per-channel K mean */
+    int smooth_v;  /* subtract the per-channel V mean (added back at the end) */
+    float v_range; /* 448 */
+} oracle_problem;
+
+/* ---- codecs ---- */
+float oracle_bf16_to_f32(uint16_t b);
+uint16_t oracle_f32_to_bf16(float x);
+float oracle_f16_to_f32(uint16_t h);
+uint16_t oracle_f32_to_f16(float x);
+float oracle_e4m3_to_f32(uint8_t b);
+uint8_t oracle_f32_to_e4m3(float x);
+int oracle_s8(float x);
+int oracle_vpos_ref(int k);
+
+/* Bulk codec helpers (n elements). */
+void oracle_decode16(const uint16_t* in, float* out, size_t n, int dtype);
+void oracle_encode16(const float* in, uint16_t* out, size_t n, int dtype);
+void oracle_e4m3_encode(const float* in, uint8_t* out, size_t n);
+void oracle_e4m3_decode(const uint8_t* in, float* out, size_t n);
+
+/* ---- splitmix64 ---- */
+uint64_t oracle_rng_next(uint64_t* state);
+double oracle_rng_uniform(uint64_t* state);
+float oracle_rng_normal(uint64_t* state);
+
+/* Synthetic Q/K/V: layout [b][t][h][d] (K and V with kv_heads heads), 16-bit
+ * codes of `dtype`. Q,V ~ N(0,1); K ~ N(0,1)*s + off[h][c], off ~ N(0, k_off_std)
+ * with s = outlier_scale on `outlier_channels` random channels per KV head;
+ * a fraction `token_frac` of tokens has Q, K and V scaled by token_scale. */
+typedef struct {
+    int batch, heads, kv_heads, tokens, head_dim, dtype;
+    float k_off_std;
+    int outlier_channels;
+    float outlier_scale;
+    float token_frac;
+    float token_scale;
+    uint64_t seed;
+} oracle_gen_spec;
+void oracle_generate(const oracle_gen_spec* s, uint16_t* q, uint16_t* k, uint16_t* v);
+
+/* The reference tests' clustered activations (tests.rs:300-329), bf16 codes,
+ * layout [b][t][h][d]. */
+void oracle_reference_synthetic(int batch, int tokens, int heads, int d, uint64_t seed, uint16_t* q, uint16_t* k,
+                                uint16_t* v);
+
+/* ---- prologue (bit-exact restatement) ----
+ * Outputs in logical layouts:
+ *   q8      [b][h][tq_pad][D]        q_scale [b][h][tq_pad/16]
+ *   k8      [b][hkv][tk_pad][D]      k_scale [b][hkv][tk_pad/64]
+ *   v8      [b][hkv][tk_pad][D]  E4M3 codes, keys in natural order
+ *   stats   [b][hkv][4][D]           K mean, V mean, V scale, 1/V scale
+ * Returns 0, or -1 for an unsupported head dim. */
+int oracle_prologue(const oracle_problem* p, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                    int8_t* q8, float* q_scale, int8_t* k8, float* k_scale, uint8_t* v8, float* stats,
+                    int threads);
+
+/* ---- attention ----
+ * `rows` (nrows entries, each < tokens) selects the query rows computed for
+ * every (b, h); NULL computes all rows. Output layout [b][h][nrows][D]. */
+
+/* Textbook softmax attention in f64 of the 16-bit inputs (reference.rs:148-184),
+ * with causal masking and grouped-query heads. */
+void oracle_attention_f64(const oracle_problem* p, int causal, float scale, const uint16_t* q,
+                          const uint16_t* k, const uint16_t* v, const int* rows, int nrows, float* out,
+                          int threads);
+
+/* The quantised algorithm on the prologue's tensors: exact int32 S, fp32
+ * online softmax in log2 units with a correctly rounded exp2, P -> E4M3,
+ * per-64-key fp32 P.V partial folded as O = O*alpha + PV, then
+ * out = O/l * v_scale + v_mean. `out` is fp32 before the final 16-bit
+ * rounding; `out16` (may be NULL) receives it rounded to `out_dtype`. */
+void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, const float* q_scale,
+                         const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* stats,
+                         const int* rows, int nrows, float* out, uint16_t* out16, int out_dtype,
+                         int threads);
+
+/* Errors of `ours` against `ref` (reference.rs:202-225):
+ * out[0] cos, [1] rel_l1, [2] rel_l2, [3] max_abs, [4] ref_max. */
+void oracle_errors(const float* ours, const float* ref, size_t n, double* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

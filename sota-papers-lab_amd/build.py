@@ -1,0 +1,73 @@
+"""Builds libsage_hip.so (the gfx950 SageAttention2 forward path) in-tree.
+
+    python sota-papers-lab_amd/build.py
+
+Compiles every source under csrc/ with hipcc for gfx950 and links
+spl_sage/libsage_hip.so next to the Python mirror of the API. Objects go to
+_build/ (git-ignored). Packed FP32 instructions are disabled for all device
+code; the prologue is compiled with -ffp-contract=off so its fp32 arithmetic
+is exactly the written operation order.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+OBJ = PKG / "_build"
+LIB = PKG / "spl_sage" / "libsage_hip.so"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+COMMON = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+PER_FILE = {
+    "sage_prologue.hip": ["-ffp-contract=off"],
+}
+SOURCES = ["sage_prologue.hip", "sage_attention.hip", "sage_peak.hip", "sage_api.cpp"]
+
+
+def _compile(src: str) -> Path:
+    out = OBJ / (src + ".o")
+    lang = ["-x", "hip"] if src.endswith(".hip") else []
+    cmd = [HIPCC, *COMMON, *PER_FILE.get(src, []), *lang, "-c", str(CSRC / src), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature and says so; that is harmless.
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src}:\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+    return out
+
+
+def build(verbose: bool = True) -> Path:
+    """Compile and link; returns the library path. Raises on failure."""
+    OBJ.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build()

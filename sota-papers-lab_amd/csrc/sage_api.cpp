@@ -1,0 +1,472 @@
+// C ABI of the gfx950 SageAttention2 forward path: the host side of the
+// reference's `spl_nn::sage` API (sezer-muhammed/sota-papers-lab,
+// platform/spl-nn/src/sage/mod.rs:116-910), re-stated in C++ over the HIP
+// runtime. Validation order and error text follow the reference so that a
+// caller sees the same failures before any launch.
+#include "../../include/sage_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "sage_device.hpp"
+#include "sage_internal.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+sage_status fail(sage_status st, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return st;
+}
+
+sage_status hip_fail(hipError_t e, const char* what) {
+    return fail(SAGE_ERR_DEVICE, "%s: %s (%s)", what, hipGetErrorName(e), hipGetErrorString(e));
+}
+
+sage_status ok() {
+    g_last_error.clear();
+    return SAGE_OK;
+}
+
+using u64 = unsigned long long;
+
+std::string shape_dbg(const sage_shape& s) {
+    char b[256];
+    if (s.kv_heads && s.kv_heads != s.heads)
+        snprintf(b, sizeof b, "Shape { batch: %llu, heads: %llu, tokens: %llu, kv_heads: %llu }", (u64)s.batch,
+                 (u64)s.heads, (u64)s.tokens, (u64)s.kv_heads);
+    else
+        snprintf(b, sizeof b, "Shape { batch: %llu, heads: %llu, tokens: %llu }", (u64)s.batch, (u64)s.heads,
+                 (u64)s.tokens);
+    return b;
+}
+
+std::string layout_dbg(const sage_frame_layout& l) {
+    char b[256];
+    snprintf(b, sizeof b, "FrameLayout { frames: %llu, special: %llu, grid_h: %llu, grid_w: %llu, dense_frames: %llu }",
+             (u64)l.frames, (u64)l.special, (u64)l.grid_h, (u64)l.grid_w, (u64)l.dense_frames);
+    return b;
+}
+
+std::string strides_dbg(const sage_strides& s) {
+    char b[160];
+    snprintf(b, sizeof b, "Strides { batch: %llu, token: %llu, head: %llu }", (u64)s.batch, (u64)s.token,
+             (u64)s.head);
+    return b;
+}
+
+std::string tile_dbg(const sage_tile& t) {
+    char b[128];
+    snprintf(b, sizeof b, "Tile { warps: %u, m_tiles: %u, stages: %u }", t.warps, t.m_tiles, t.stages);
+    return b;
+}
+
+uint64_t div_ceil(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+uint64_t round_up(uint64_t a, uint64_t m) { return div_ceil(a, m) * m; }
+
+// FrameLayout::tokens_per_frame / merged_per_frame / merged_keys (mod.rs:284-300).
+uint64_t tokens_per_frame(const sage_frame_layout& l) { return l.special + l.grid_h * l.grid_w; }
+uint64_t merged_per_frame(const sage_frame_layout& l, uint64_t s) {
+    return l.special + div_ceil(l.grid_h, s) * div_ceil(l.grid_w, s);
+}
+uint64_t merged_keys(const sage_frame_layout& l, uint64_t s) {
+    const uint64_t d = l.dense_frames < l.frames ? l.dense_frames : l.frames;
+    return d * tokens_per_frame(l) + (l.frames - d) * merged_per_frame(l, s);
+}
+
+// `int` (mod.rs:387-389).
+bool fits_i32(uint64_t v, const char* what, sage_status* st) {
+    if (v > 2147483647ull) {
+        *st = fail(SAGE_ERR_INVALID, "%s = %llu does not fit in i32", what, (u64)v);
+        return false;
+    }
+    return true;
+}
+
+uint64_t kv_heads_of(const sage_shape& s) { return s.kv_heads ? s.kv_heads : s.heads; }
+
+}  // namespace
+
+struct sage_attention {
+    hipStream_t stream;
+    int device;
+    uint64_t head_dim;
+    sage_config config;
+};
+
+struct sage_workspace {
+    sage_plan plan;
+    uint64_t head_dim;
+    int device;
+    int8_t* q8 = nullptr;
+    float* q_scale = nullptr;
+    int8_t* k8 = nullptr;
+    float* k_scale = nullptr;
+    uint8_t* v8 = nullptr;
+    float* stats = nullptr;
+    float* kbias = nullptr;
+    float* part = nullptr;
+    uint64_t n_q8 = 0, n_q_scale = 0, n_k8 = 0, n_k_scale = 0, n_v8 = 0, n_stats = 0, n_kbias = 0, n_part = 0;
+    bool prepared = false;
+    sage::Geom geom{};
+};
+
+extern "C" {
+
+const char* sage_last_error(void) { return g_last_error.c_str(); }
+
+sage_status sage_plan_new(const sage_shape* shape, const sage_kv_merge* merge, sage_plan* out) {
+    if (!shape || !merge || !out) return fail(SAGE_ERR_INVALID, "null argument");
+    const sage_shape& s = *shape;
+    if (s.batch == 0 || s.heads == 0 || s.tokens == 0)
+        return fail(SAGE_ERR_INVALID, "empty attention shape %s", shape_dbg(s).c_str());
+    const uint64_t hk = kv_heads_of(s);
+    if (s.heads % hk != 0)
+        return fail(SAGE_ERR_INVALID, "%llu query heads are not a multiple of %llu KV heads", (u64)s.heads, (u64)hk);
+    uint64_t tk;
+    if (merge->stride == 1) {
+        tk = s.tokens;
+    } else {
+        if (merge->stride != 2 && merge->stride != 4)
+            return fail(SAGE_ERR_INVALID, "KV merge stride must be 2 or 4, got %u", merge->stride);
+        const sage_frame_layout& l = merge->layout;
+        if (l.grid_h == 0 || l.grid_w == 0)
+            return fail(SAGE_ERR_INVALID, "KV merge needs a patch grid: %s", layout_dbg(l).c_str());
+        if (l.frames * tokens_per_frame(l) != s.tokens)
+            return fail(SAGE_ERR_INVALID, "frame layout %s covers %llu tokens, the sequence has %llu",
+                        layout_dbg(l).c_str(), (u64)(l.frames * tokens_per_frame(l)), (u64)s.tokens);
+        tk = merged_keys(l, merge->stride);
+    }
+    sage_plan p{};
+    p.shape = s;
+    p.shape.kv_heads = hk;
+    p.merge = *merge;
+    p.tq_pad = round_up(s.tokens, SAGE_QTILE);
+    p.tk = tk;
+    p.tk_pad = round_up(tk, SAGE_KBLOCK);
+    sage_status st = SAGE_OK;
+    if (!fits_i32(p.tq_pad, "padded queries", &st) || !fits_i32(p.tk_pad, "padded keys", &st) ||
+        !fits_i32(s.batch * s.heads, "batch × heads", &st))
+        return st;
+    *out = p;
+    return ok();
+}
+
+double sage_flops(const sage_plan* plan, uint64_t head_dim, int32_t causal) {
+    if (!plan) return 0.0;
+    const double bh = (double)(plan->shape.batch * plan->shape.heads);
+    if (causal) return 2.0 * bh * (double)head_dim * (double)plan->shape.tokens * ((double)plan->shape.tokens + 1.0);
+    return 4.0 * bh * (double)plan->shape.tokens * (double)plan->tk * (double)head_dim;
+}
+
+sage_status sage_strides_check(const sage_strides* s, const char* what) {
+    if (!s) return fail(SAGE_ERR_INVALID, "null strides");
+    if (s->batch % 8 || s->token % 8 || s->head % 8)
+        return fail(SAGE_ERR_INVALID, "%s strides must be multiples of 8 elements: %s", what ? what : "tensor",
+                    strides_dbg(*s).c_str());
+    return ok();
+}
+
+uint64_t sage_strides_extent(const sage_strides* s, uint64_t batch, uint64_t tokens, uint64_t heads,
+                             uint64_t head_dim) {
+    if (!s || batch == 0 || tokens == 0 || heads == 0) return 0;
+    return (batch - 1) * s->batch + (tokens - 1) * s->token + (heads - 1) * s->head + head_dim;
+}
+
+// This build's tile menu: 4 wave64s of one 32-query MFMA tile each, two K/V
+// LDS buffers (128 rows per workgroup).
+sage_status sage_tile_validate(const sage_tile* t) {
+    if (!t) return fail(SAGE_ERR_INVALID, "null tile");
+    if (t->warps != 4 || t->m_tiles != 1 || t->stages != 2)
+        return fail(SAGE_ERR_INVALID, "unsupported sage tile %s", tile_dbg(*t).c_str());
+    return ok();
+}
+
+sage_config sage_config_for_head_dim(uint64_t head_dim) {
+    (void)head_dim;
+    sage_config c{};
+    c.tile.warps = 4;
+    c.tile.m_tiles = 1;
+    c.tile.stages = 2;
+    c.pv_accum = SAGE_PV_F32;
+    return c;
+}
+
+sage_status sage_check_device(int ordinal) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return hip_fail(e, "device count");
+    if (ordinal < 0 || ordinal >= n)
+        return fail(SAGE_ERR_DEVICE, "no HIP device %d (%d visible)", ordinal, n);
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, ordinal);
+    if (e != hipSuccess) return hip_fail(e, "device properties");
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(SAGE_ERR_DEVICE,
+                    "sage attention needs INT8 and FP8 MFMA of an MI355X-class GPU (gfx950); this GPU is %s",
+                    p.gcnArchName);
+    return ok();
+}
+
+sage_status sage_new(void* stream, uint64_t head_dim, const sage_config* config, sage_attention** out) {
+    if (!out) return fail(SAGE_ERR_INVALID, "null output");
+    *out = nullptr;
+    if (head_dim != 64 && head_dim != 128)
+        return fail(SAGE_ERR_INVALID, "sage attention supports head dim 64 or 128, got %llu", (u64)head_dim);
+    const sage_config cfg = config ? *config : sage_config_for_head_dim(head_dim);
+    sage_status st = sage_tile_validate(&cfg.tile);
+    if (st != SAGE_OK) return st;
+    if (cfg.pv_accum == SAGE_PV_F16)
+        return fail(SAGE_ERR_UNSUPPORTED, "FP16 P.V accumulation (PvAccum::F16) is not supported by this build");
+    if (cfg.pv_accum != SAGE_PV_F32) return fail(SAGE_ERR_INVALID, "unknown PvAccum %d", cfg.pv_accum);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "current device");
+    st = sage_check_device(dev);
+    if (st != SAGE_OK) return st;
+    sage_attention* s = new sage_attention;
+    s->stream = static_cast<hipStream_t>(stream);
+    s->device = dev;
+    s->head_dim = head_dim;
+    s->config = cfg;
+    *out = s;
+    return ok();
+}
+
+void sage_destroy(sage_attention* s) { delete s; }
+uint64_t sage_head_dim(const sage_attention* s) { return s ? s->head_dim : 0; }
+sage_config sage_get_config(const sage_attention* s) { return s ? s->config : sage_config{}; }
+void* sage_stream(const sage_attention* s) { return s ? static_cast<void*>(s->stream) : nullptr; }
+
+sage_status sage_attn_resources(const sage_attention* s, int32_t* regs, int32_t* spill, int32_t* lds) {
+    if (!s || !regs || !spill || !lds) return fail(SAGE_ERR_INVALID, "null argument");
+    int r = 0, sp = 0, l = 0;
+    hipError_t e = sage::attention_resources((int)s->head_dim, false, &r, &sp, &l);
+    if (e != hipSuccess) return hip_fail(e, "registers");
+    *regs = r;
+    *spill = sp;
+    *lds = l;
+    return ok();
+}
+
+static void ws_free(sage_workspace* w) {
+    void* bufs[] = {w->q8, w->q_scale, w->k8, w->k_scale, w->v8, w->stats, w->kbias, w->part};
+    for (void* p : bufs)
+        if (p) (void)hipFree(p);
+}
+
+sage_status sage_workspace_new(const sage_attention* s, const sage_shape* shape, const sage_kv_merge* merge,
+                           sage_workspace** out) {
+    if (!s || !shape || !out) return fail(SAGE_ERR_INVALID, "null argument");
+    *out = nullptr;
+    sage_kv_merge dense{};
+    dense.stride = 1;
+    sage_plan plan;
+    sage_status st = sage_plan_new(shape, merge ? merge : &dense, &plan);
+    if (st != SAGE_OK) return st;
+    if (plan.merge.stride != 1)
+        return fail(SAGE_ERR_UNSUPPORTED, "KV merging (KvMerge::Pool) is not supported by this build");
+    const uint64_t b = plan.shape.batch, h = plan.shape.heads, hk = plan.shape.kv_heads, d = s->head_dim;
+    sage_workspace* w = new sage_workspace;
+    w->plan = plan;
+    w->head_dim = d;
+    w->device = s->device;
+    w->n_q8 = b * h * plan.tq_pad * d;
+    w->n_q_scale = b * h * plan.tq_pad / SAGE_QGROUP;
+    w->n_k8 = b * hk * plan.tk_pad * d;
+    w->n_k_scale = b * hk * plan.tk_pad / SAGE_KBLOCK;
+    w->n_v8 = b * hk * plan.tk_pad * d;
+    w->n_stats = b * hk * 4 * d;
+    w->n_kbias = plan.tk_pad;
+    w->n_part = b * hk * (plan.tq_pad / SAGE_QTILE) * 4 * d;
+    struct {
+        void** p;
+        uint64_t bytes;
+    } allocs[] = {
+        {(void**)&w->q8, w->n_q8},       {(void**)&w->q_scale, w->n_q_scale * 4}, {(void**)&w->k8, w->n_k8},
+        {(void**)&w->k_scale, w->n_k_scale * 4}, {(void**)&w->v8, w->n_v8},       {(void**)&w->stats, w->n_stats * 4},
+        {(void**)&w->kbias, w->n_kbias * 4},     {(void**)&w->part, w->n_part * 4},
+    };
+    for (auto& a : allocs) {
+        hipError_t e = hipMalloc(a.p, a.bytes);
+        if (e == hipSuccess) e = hipMemsetAsync(*a.p, 0, a.bytes, s->stream);
+        if (e != hipSuccess) {
+            ws_free(w);
+            delete w;
+            return hip_fail(e, "allocate sage workspace");
+        }
+    }
+    *out = w;
+    return ok();
+}
+
+void sage_workspace_destroy(sage_workspace* ws) {
+    if (!ws) return;
+    ws_free(ws);
+    delete ws;
+}
+
+uint64_t sage_workspace_bytes(const sage_workspace* w) {
+    if (!w) return 0;
+    return w->n_q8 + 4 * w->n_q_scale + w->n_k8 + 4 * w->n_k_scale + w->n_v8 + 4 * w->n_stats + 4 * w->n_kbias +
+           4 * w->n_part;
+}
+
+sage_status sage_workspace_plan(const sage_workspace* ws, sage_plan* out) {
+    if (!ws || !out) return fail(SAGE_ERR_INVALID, "null argument");
+    *out = ws->plan;
+    return ok();
+}
+
+sage_status sage_workspace_buffers(const sage_workspace* w, sage_ws_buffers* out) {
+    if (!w || !out) return fail(SAGE_ERR_INVALID, "null argument");
+    out->q8 = w->q8;
+    out->q_scale = w->q_scale;
+    out->k8 = w->k8;
+    out->k_scale = w->k_scale;
+    out->v8 = w->v8;
+    out->stats = w->stats;
+    out->kbias = w->kbias;
+    out->q8_len = w->n_q8;
+    out->q_scale_len = w->n_q_scale;
+    out->k8_len = w->n_k8;
+    out->k_scale_len = w->n_k_scale;
+    out->v8_len = w->n_v8;
+    out->stats_len = w->n_stats;
+    out->kbias_len = w->n_kbias;
+    return ok();
+}
+
+static sage_status check_tensor(const sage_strides& st, const void* data, uint64_t len, const sage_plan& plan,
+                                uint64_t heads, uint64_t d, const char* what) {
+    sage_status r = sage_strides_check(&st, what);
+    if (r != SAGE_OK) return r;
+    const uint64_t need = sage_strides_extent(&st, plan.shape.batch, plan.shape.tokens, heads, d);
+    if (len < need)
+        return fail(SAGE_ERR_INVALID, "%s holds %llu elements, its shape and strides need %llu", what, (u64)len,
+                    (u64)need);
+    if (!data || (reinterpret_cast<uintptr_t>(data) & 15u))
+        return fail(SAGE_ERR_INVALID, "%s must start at a 16-byte aligned device address", what);
+    return SAGE_OK;
+}
+
+sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,
+                         const sage_tensor* v, const sage_options* opts) {
+    if (!s || !ws || !q || !k || !v || !opts) return fail(SAGE_ERR_INVALID, "null argument");
+    if (ws->head_dim != s->head_dim)
+        return fail(SAGE_ERR_INVALID, "workspace was made for head dim %llu, kernels are %llu", (u64)ws->head_dim,
+                    (u64)s->head_dim);
+    const sage_plan& plan = ws->plan;
+    const uint64_t d = s->head_dim;
+    const struct {
+        const sage_tensor* t;
+        uint64_t heads;
+        const char* what;
+    } ins[] = {{q, plan.shape.heads, "Q"}, {k, plan.shape.kv_heads, "K"}, {v, plan.shape.kv_heads, "V"}};
+    for (auto& in : ins) {
+        sage_status r = check_tensor(in.t->strides, in.t->data, in.t->len, plan, in.heads, d, in.what);
+        if (r != SAGE_OK) return r;
+    }
+    if (q->dtype != k->dtype || q->dtype != v->dtype)
+        return fail(SAGE_ERR_INVALID, "Q, K and V must share one element type");
+    if (q->dtype != SAGE_BF16 && q->dtype != SAGE_F16) return fail(SAGE_ERR_INVALID, "unknown dtype %d", q->dtype);
+    if (opts->qk_norm_params) {
+        if (opts->qk_norm_len < 4 * d)
+            return fail(SAGE_ERR_INVALID, "QK-norm params hold %llu floats, need %llu", (u64)opts->qk_norm_len,
+                        (u64)(4 * d));
+        return fail(SAGE_ERR_UNSUPPORTED, "the fused QK LayerNorm (QkNorm) is not supported by this build");
+    }
+    int flags = 0;
+    if (opts->smooth_k) flags |= sage::F_SMOOTH_K;
+    if (opts->smooth_v) flags |= sage::F_SMOOTH_V;
+    if (opts->causal) flags |= sage::F_CAUSAL;
+    if (q->dtype == SAGE_F16) flags |= sage::F_IN_F16;
+    const float scale = opts->has_softmax_scale ? opts->softmax_scale : 1.0f / std::sqrt((float)d);
+    const float log2e = 1.44269504088896340736f;
+
+    sage::Geom g{};
+    g.q_sb = (long long)q->strides.batch;
+    g.q_st = (long long)q->strides.token;
+    g.q_sh = (long long)q->strides.head;
+    g.k_sb = (long long)k->strides.batch;
+    g.k_st = (long long)k->strides.token;
+    g.k_sh = (long long)k->strides.head;
+    g.v_sb = (long long)v->strides.batch;
+    g.v_st = (long long)v->strides.token;
+    g.v_sh = (long long)v->strides.head;
+    g.batch = (int)plan.shape.batch;
+    g.heads = (int)plan.shape.heads;
+    g.kv_heads = (int)plan.shape.kv_heads;
+    g.group = (int)(plan.shape.heads / plan.shape.kv_heads);
+    g.tokens = (int)plan.shape.tokens;
+    g.tq_pad = (int)plan.tq_pad;
+    g.tk = (int)plan.tk;
+    g.tk_pad = (int)plan.tk_pad;
+    g.q_tiles = (int)(plan.tq_pad / SAGE_QTILE);
+    g.kblocks = (int)(plan.tk_pad / SAGE_KBLOCK);
+    g.flags = flags;
+    g.q_mul = scale * log2e;
+    g.v_range = SAGE_FP8_MAX;
+
+    sage::PrologueBufs bufs{ws->q8, ws->q_scale, ws->k8, ws->k_scale, ws->v8, ws->stats, ws->part};
+    hipError_t e = sage::launch_prologue((int)d, static_cast<const uint16_t*>(q->data),
+                                         static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
+                                         bufs, g, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "launch sage prologue");
+    ws->geom = g;
+    ws->prepared = true;
+    return ok();
+}
+
+sage_status sage_attend(const sage_attention* s, const sage_workspace* ws, const sage_tensor_mut* out) {
+    if (!s || !ws || !out) return fail(SAGE_ERR_INVALID, "null argument");
+    if (!ws->prepared) return fail(SAGE_ERR_STATE, "sage workspace has not been prepared");
+    if (ws->head_dim != s->head_dim)
+        return fail(SAGE_ERR_INVALID, "workspace was made for head dim %llu, kernels are %llu", (u64)ws->head_dim,
+                    (u64)s->head_dim);
+    const sage_plan& plan = ws->plan;
+    sage_status r = check_tensor(out->strides, out->data, out->len, plan, plan.shape.heads, s->head_dim, "output");
+    if (r != SAGE_OK) return r;
+    if (out->dtype != SAGE_BF16 && out->dtype != SAGE_F16)
+        return fail(SAGE_ERR_INVALID, "unknown dtype %d", out->dtype);
+    sage::Geom g = ws->geom;
+    g.o_sb = (long long)out->strides.batch;
+    g.o_st = (long long)out->strides.token;
+    g.o_sh = (long long)out->strides.head;
+    g.flags = (g.flags & ~sage::F_OUT_F16) | (out->dtype == SAGE_F16 ? sage::F_OUT_F16 : 0);
+    sage::AttendBufs bufs{ws->q8, ws->q_scale, ws->k8, ws->k_scale, ws->v8, ws->stats, out->data};
+    hipError_t e = sage::launch_attention((int)s->head_dim, bufs, g, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "launch sage attention");
+    return ok();
+}
+
+sage_status sage_forward(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,
+                         const sage_tensor* v, const sage_tensor_mut* out, const sage_options* opts) {
+    sage_status r = sage_prepare(s, ws, q, k, v, opts);
+    if (r != SAGE_OK) return r;
+    return sage_attend(s, ws, out);
+}
+
+int32_t sage_v8_position(int32_t k) { return (k < 0 || k >= SAGE_KBLOCK) ? -1 : sage::v8_position(k); }
+
+sage_status sage_peak(const sage_attention* s, int32_t which, int32_t iters, double* tops) {
+    if (!s || !tops) return fail(SAGE_ERR_INVALID, "null argument");
+    if (which < 0 || which > 2) return fail(SAGE_ERR_INVALID, "unknown peak probe %d", which);
+    if (iters <= 0) return fail(SAGE_ERR_INVALID, "peak probe needs iters > 0");
+    hipError_t e = sage::run_peak(which, iters, s->stream, tops);
+    if (e != hipSuccess) return hip_fail(e, "peak probe");
+    return ok();
+}
+
+}  // extern "C"

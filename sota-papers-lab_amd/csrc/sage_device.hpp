@@ -1,0 +1,116 @@
+// Device-side definitions shared by the SageAttention2 kernels for gfx950:
+// the parameter block, the bit-exact codecs of the prologue and MFMA vector
+// types. Reference semantics: sezer-muhammed/sota-papers-lab,
+// platform/spl-nn/cuda/sage_common.cu (codecs :66-99) and src/sage/reference.rs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sage {
+
+constexpr int QGROUP = 16;  // query rows per INT8 Q scale
+constexpr int QTILE = 128;  // queries per prologue tile (one K/V statistics partial)
+constexpr int KBLOCK = 64;  // keys per K scale and per V block
+
+enum : int {
+    F_SMOOTH_K = 4,  // flag values of the reference's SgGeom::flags (sage_common.cu:26-29)
+    F_SMOOTH_V = 8,
+    F_CAUSAL = 16,   // extensions
+    F_IN_F16 = 32,
+    F_OUT_F16 = 64,
+};
+
+// Kernel parameter block, passed by value. Element strides of the 16-bit
+// [batch][token][head][dim] inputs and output; channels contiguous.
+struct Geom {
+    long long q_sb, q_st, q_sh;
+    long long k_sb, k_st, k_sh;
+    long long v_sb, v_st, v_sh;
+    long long o_sb, o_st, o_sh;
+    int batch, heads, kv_heads, group;  // group = heads / kv_heads
+    int tokens;                         // queries and keys per batch item
+    int tq_pad, tk, tk_pad;             // tokens rounded to QTILE; keys; keys rounded to KBLOCK
+    int q_tiles, kblocks;               // tq_pad / QTILE, tk_pad / KBLOCK
+    int flags;
+    float q_mul;    // softmax scale * log2(e), folded into the Q scales
+    float v_range;  // max |V - mean| maps to this E4M3 value (448)
+};
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
+}
+
+// Eight 16-bit values of one 16-byte vector -> floats.
+__device__ __forceinline__ void unpack8(uint4 v, float* f, bool f16) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (f16) {
+            f[2 * i] = f16_to_f32(w[i] & 0xffffu);
+            f[2 * i + 1] = f16_to_f32(w[i] >> 16);
+        } else {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+}
+
+// Round to nearest even, clamp to +-127 (sage_common.cu:95-99; NaN -> 0).
+__device__ __forceinline__ uint32_t s8_code(float x) {
+    float r = __builtin_rintf(x);
+    r = r != r ? 0.f : fminf(fmaxf(r, -127.f), 127.f);
+    return (uint32_t)((int)r) & 0xffu;
+}
+
+__device__ __forceinline__ uint32_t s8x4(float a, float b, float c, float d) {
+    return s8_code(a) | (s8_code(b) << 8) | (s8_code(c) << 16) | (s8_code(d) << 24);
+}
+
+// f32 -> E4M3 (OCP e4m3fn), round to nearest even, saturating at +-448, NaN
+// -> 0x7f: the semantics of reference.rs:40-70 (cvt.rn.satfinite). Done on the
+// bit pattern so that it is exact for every input, including the NaN code.
+__device__ __forceinline__ uint32_t e4m3_code(float x) {
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return 0x7fu;
+    if (a >= 0x43e00000u) return sign | 0x7eu;  // |x| >= 448
+    if (a >= 0x3c800000u)                       // |x| >= 2^-6: keep 3 mantissa bits
+        return sign | (((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - (120u << 3));
+    return sign | (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);  // k * 2^-9, k <= 8
+}
+
+// f32 -> bf16 bits, round to nearest even, NaN kept (reference.rs:13-20).
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if (x != x) return (u >> 16) | 0x40u;
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ uint32_t f16_bits(float x) {
+    return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)x);
+}
+
+// Byte position of key k (0..63) of a 64-key block inside each channel row of
+// the V tile. The 32x32 INT8 MFMA leaves key 32t + 8j + 4g + r of a column
+// in lane-half g, accumulator 4j + r of sub-tile t; packed four to a register
+// that is byte 16t + 4j + r of lane-half g's 32-byte FP8 operand, so V's
+// channel rows store that key at byte 32g + 16t + 4j + r.
+__host__ __device__ __forceinline__ int v8_position(int k) {
+    return 32 * ((k >> 2) & 1) + 16 * (k >> 5) + 4 * ((k >> 3) & 3) + (k & 3);
+}
+
+// XOR swizzle of 16-byte chunk u inside 128-byte lines of an LDS tile: lanes
+// that read one chunk column of eight consecutive rows hit eight different
+// bank groups.
+__device__ __forceinline__ int swz(int u) { return (u & ~7) | ((u ^ (u >> 3)) & 7); }
+
+}  // namespace sage

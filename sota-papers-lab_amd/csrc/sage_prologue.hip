@@ -1,0 +1,300 @@
+// SageAttention2 prologue for gfx950: K/V channel statistics, INT8 Q (one
+// scale per 16 rows), INT8 K (one scale per 64 keys), FP8 E4M3 V (one scale
+// per channel). Three HBM-bound launches:
+//
+//   sage_prep      grid (q_tiles, kv_heads, batch): per 128-token tile, the
+//                  partial K sum, V sum, V min, V max of every channel, and
+//                  INT8 Q of the `group` query heads that share the KV head
+//   sage_finalize  grid (kv_heads, batch): K mean, V mean, V scale, 1/V scale
+//   sage_quant_kv  grid (kblocks, kv_heads, batch): smoothed INT8 K and FP8 V,
+//                  V transposed per 64-key block into the MFMA operand order
+//
+// Codes and scales are bit-identical to the reference's
+// (sezer-muhammed/sota-papers-lab, platform/spl-nn/cuda/sage_quant.cu:59-206,
+// 238-319): each fp32 sum keeps that kernel's operation order, which is fixed
+// by its 256-thread tile, its 32-lane warp butterfly and its even/odd tile
+// fold. A 256-thread workgroup here is four wave64s; each 32-lane half of a
+// wave plays one of the reference's warps, so the same partials meet in the
+// same order.
+#include "sage_device.hpp"
+#include "sage_internal.hpp"
+
+namespace sage {
+
+__device__ __forceinline__ uint4 load16(const uint16_t* p, bool ok) {
+    return ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// sage_quant.cu:59-160 (sg_prep), without LayerNorm.
+template <int D>
+__global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                 const uint16_t* __restrict__ v, int8_t* __restrict__ q8,
+                                                 float* __restrict__ q_scale, float* __restrict__ part, Geom g) {
+    constexpr int CH = D / 8;        // 16-byte chunks per head row
+    constexpr int TPI = 256 / CH;    // tokens per iteration
+    constexpr int NI = QTILE / TPI;  // iterations
+    const int tile = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, ch = tid % CH, slot = tid / CH;
+    const bool f16 = g.flags & F_IN_F16;
+    const long long bhk = (long long)b * g.kv_heads + hk;
+
+    __shared__ unsigned gmax[QTILE / QGROUP];
+    __shared__ float red[8][4][D];
+
+    // K and V channel statistics of this tile's tokens.
+    float ks[8], vs[8], vmn[8], vmx[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        ks[e] = 0.f;
+        vs[e] = 0.f;
+        vmn[e] = 3.0e38f;
+        vmx[e] = -3.0e38f;
+    }
+    uint4 kraw[NI], vraw[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int tok = tile * QTILE + slot + i * TPI;
+        const bool ok = tok < g.tokens;
+        kraw[i] = load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, ok);
+        vraw[i] = load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, ok);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int tok = tile * QTILE + slot + i * TPI;
+        if (tok < g.tokens) {
+            float fk[8], fv[8];
+            unpack8(kraw[i], fk, f16);
+            unpack8(vraw[i], fv, f16);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                ks[e] += fk[e];
+                vs[e] += fv[e];
+                vmn[e] = fminf(vmn[e], fv[e]);
+                vmx[e] = fmaxf(vmx[e], fv[e]);
+            }
+        }
+    }
+    // Lanes of one 32-lane half that hold the same channels, then the halves
+    // in order (sage_quant.cu:129-159).
+#pragma unroll
+    for (int o = CH; o < 32; o <<= 1) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            ks[e] += __shfl_xor(ks[e], o, 64);
+            vs[e] += __shfl_xor(vs[e], o, 64);
+            vmn[e] = fminf(vmn[e], __shfl_xor(vmn[e], o, 64));
+            vmx[e] = fmaxf(vmx[e], __shfl_xor(vmx[e], o, 64));
+        }
+    }
+    if ((tid & 31) < CH) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            red[tid >> 5][0][ch * 8 + e] = ks[e];
+            red[tid >> 5][1][ch * 8 + e] = vs[e];
+            red[tid >> 5][2][ch * 8 + e] = vmn[e];
+            red[tid >> 5][3][ch * 8 + e] = vmx[e];
+        }
+    }
+    __syncthreads();
+    for (int c = tid; c < 4 * D; c += 256) {
+        const int stat = c / D, d = c % D;
+        float r = red[0][stat][d];
+#pragma unroll
+        for (int w = 1; w < 8; w++) {
+            const float x = red[w][stat][d];
+            r = stat < 2 ? r + x : (stat == 2 ? fminf(r, x) : fmaxf(r, x));
+        }
+        part[((bhk * g.q_tiles + tile) * 4 + stat) * D + d] = r;
+    }
+
+    // INT8 Q of every query head that reads this KV head (sage_quant.cu:85-127).
+    for (int gi = 0; gi < g.group; gi++) {
+        const int h = hk * g.group + gi;
+        const long long bh = (long long)b * g.heads + h;
+        if (tid < QTILE / QGROUP) gmax[tid] = 0u;
+        __syncthreads();
+        uint4 qraw[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int tok = tile * QTILE + slot + i * TPI;
+            qraw[i] = load16(q + b * g.q_sb + (long long)tok * g.q_st + h * g.q_sh + ch * 8, tok < g.tokens);
+        }
+        float qv[NI][8];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            unpack8(qraw[i], qv[i], f16);
+            float amax = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(qv[i][e]));
+            // A wave's tokens of one iteration lie in one 16-row group.
+            amax = wave_max(amax);
+            if ((tid & 63) == 0) atomicMax(&gmax[(slot + i * TPI) / QGROUP], __float_as_uint(amax));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int tl = slot + i * TPI;
+            const float amax = __uint_as_float(gmax[tl / QGROUP]);
+            const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+            const float* f = qv[i];
+            uint2 w;
+            w.x = s8x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
+            w.y = s8x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
+            *reinterpret_cast<uint2*>(q8 + (bh * g.tq_pad + tile * QTILE + tl) * D + ch * 8) = w;
+        }
+        if (tid < QTILE / QGROUP)
+            q_scale[bh * (g.tq_pad / QGROUP) + tile * (QTILE / QGROUP) + tid] =
+                __uint_as_float(gmax[tid]) * (1.0f / 127.0f) * g.q_mul;
+        __syncthreads();
+    }
+}
+
+// sage_quant.cu:163-206 (sg_finalize): even and odd tiles folded separately.
+template <int D>
+__global__ __launch_bounds__(256) void sage_finalize(const float* __restrict__ part, float* __restrict__ stats,
+                                                     Geom g) {
+    const int hk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const long long bhk = (long long)b * g.kv_heads + hk;
+    __shared__ float st[4][D];
+    for (int c = tid; c < 4 * D; c += 256) {
+        const int stat = c / D, d = c % D;
+        const float* p = part + bhk * g.q_tiles * 4 * D + stat * D + d;
+        float r0 = stat < 2 ? 0.f : (stat == 2 ? 3.0e38f : -3.0e38f);
+        float r1 = r0;
+        int t = 0;
+        for (; t + 1 < g.q_tiles; t += 2) {
+            const float x0 = p[(long long)t * 4 * D], x1 = p[(long long)(t + 1) * 4 * D];
+            if (stat < 2) {
+                r0 += x0;
+                r1 += x1;
+            } else if (stat == 2) {
+                r0 = fminf(r0, x0);
+                r1 = fminf(r1, x1);
+            } else {
+                r0 = fmaxf(r0, x0);
+                r1 = fmaxf(r1, x1);
+            }
+        }
+        if (t < g.q_tiles) {
+            const float x0 = p[(long long)t * 4 * D];
+            r0 = stat < 2 ? r0 + x0 : (stat == 2 ? fminf(r0, x0) : fmaxf(r0, x0));
+        }
+        st[stat][d] = stat < 2 ? r0 + r1 : (stat == 2 ? fminf(r0, r1) : fmaxf(r0, r1));
+    }
+    __syncthreads();
+    for (int d = tid; d < D; d += 256) {
+        const float n = (float)g.tokens;
+        const float mk = (g.flags & F_SMOOTH_K) ? st[0][d] / n : 0.f;
+        const float mv = (g.flags & F_SMOOTH_V) ? st[1][d] / n : 0.f;
+        const float amax = fmaxf(st[3][d] - mv, mv - st[2][d]);
+        const float scale = amax > 0.f ? amax / g.v_range : 1.0f;
+        float* o = stats + bhk * 4 * D;
+        o[d] = mk;
+        o[D + d] = mv;
+        o[2 * D + d] = scale;
+        o[3 * D + d] = 1.0f / scale;
+    }
+}
+
+// sage_quant.cu:238-319 (sg_quant_kv), dense: K - mean -> INT8 per block,
+// (V - mean) / scale -> E4M3, V stored [block][channel][v8_position(key)].
+template <int D>
+__global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                                     const float* __restrict__ stats, int8_t* __restrict__ k8,
+                                                     float* __restrict__ k_scale, uint8_t* __restrict__ v8, Geom g) {
+    constexpr int CH = D / 8;
+    constexpr int TPI = 256 / CH;
+    constexpr int NI = KBLOCK / TPI;
+    const int blk = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, ch = tid % CH, slot = tid / CH;
+    const bool f16 = g.flags & F_IN_F16;
+    const long long bhk = (long long)b * g.kv_heads + hk;
+
+    __shared__ unsigned kmax;
+    __shared__ __attribute__((aligned(16))) uint8_t vt[D * KBLOCK];
+    if (tid == 0) kmax = 0u;
+
+    const float* st = stats + bhk * 4 * D;
+    float mk[8], mv[8], iv[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        mk[e] = st[ch * 8 + e];
+        mv[e] = st[D + ch * 8 + e];
+        iv[e] = st[3 * D + ch * 8 + e];
+    }
+    uint4 kraw[NI], vraw[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int j = blk * KBLOCK + slot + i * TPI;
+        const bool ok = j < g.tk;
+        kraw[i] = load16(k + b * g.k_sb + (long long)j * g.k_st + hk * g.k_sh + ch * 8, ok);
+        vraw[i] = load16(v + b * g.v_sb + (long long)j * g.v_st + hk * g.v_sh + ch * 8, ok);
+    }
+    __syncthreads();
+    float kv[NI][8];
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int kl = slot + i * TPI;
+        const bool ok = blk * KBLOCK + kl < g.tk;
+        float fk[8], fv[8];
+        unpack8(kraw[i], fk, f16);
+        unpack8(vraw[i], fv, f16);
+        const int pos = v8_position(kl);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            // The reference sums the (one) member from 0.0f first: -0 becomes +0.
+            kv[i][e] = ok ? (fk[e] + 0.0f) - mk[e] : 0.f;
+            amax = fmaxf(amax, fabsf(kv[i][e]));
+            const float vq = ok ? ((fv[e] + 0.0f) - mv[e]) * iv[e] : 0.f;
+            vt[(ch * 8 + e) * KBLOCK + pos] = (uint8_t)e4m3_code(vq);
+        }
+    }
+    amax = wave_max(amax);
+    if ((tid & 63) == 0) atomicMax(&kmax, __float_as_uint(amax));
+    __syncthreads();
+
+    const float km = __uint_as_float(kmax);
+    const float inv = km > 0.f ? 127.0f / km : 0.f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int kl = slot + i * TPI;
+        const float* f = kv[i];
+        uint2 w;
+        w.x = s8x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
+        w.y = s8x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
+        *reinterpret_cast<uint2*>(k8 + (bhk * g.tk_pad + blk * KBLOCK + kl) * D + ch * 8) = w;
+    }
+    if (tid == 0) k_scale[bhk * g.kblocks + blk] = km * (1.0f / 127.0f);
+    uint8_t* vo = v8 + (bhk * g.kblocks + blk) * (long long)(D * KBLOCK);
+    for (int c = tid; c < D * KBLOCK / 16; c += 256)
+        reinterpret_cast<uint4*>(vo)[c] = reinterpret_cast<const uint4*>(vt)[c];
+}
+
+template <int D>
+static hipError_t launch_prologue_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, const PrologueBufs& w,
+                                    const Geom& g, hipStream_t s) {
+    hipLaunchKernelGGL(sage_prep<D>, dim3(g.q_tiles, g.kv_heads, g.batch), dim3(256), 0, s, q, k, v, w.q8,
+                       w.q_scale, w.part, g);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(sage_finalize<D>, dim3(g.kv_heads, g.batch), dim3(256), 0, s, w.part, w.stats, g);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(sage_quant_kv<D>, dim3(g.kblocks, g.kv_heads, g.batch), dim3(256), 0, s, k, v, w.stats, w.k8,
+                       w.k_scale, w.v8, g);
+    return hipGetLastError();
+}
+
+hipError_t launch_prologue(int head_dim, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                           const PrologueBufs& w, const Geom& g, hipStream_t s) {
+    return head_dim == 64 ? launch_prologue_d<64>(q, k, v, w, g, s) : launch_prologue_d<128>(q, k, v, w, g, s);
+}
+
+}  // namespace sage

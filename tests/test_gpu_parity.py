@@ -1,0 +1,120 @@
+"""Parity of the HIP path with the oracle, through the C ABI.
+
+Prologue codes, scales and statistics must be bit-exact. The attention output
+is gated, as the north star states, at cosine >= 0.999 and max-abs <= 2e-2
+against the oracle's restatement of the reference's quantised arithmetic
+(sage emulator). Against exact f64 attention the output may be no further
+than the reference arithmetic itself is (plus a small slack): on unclustered
+N(0,1) inputs the algorithm's own error sits near cos 0.9988, so the
+reference's fixed gate (cos > 0.999, rel_l2 < 0.04, tests.rs:699) is applied
+on the reference's own clustered test data in test_gpu_reference_ports.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from sage_gpu_helpers import assert_prologue_equal, gather_rows, run, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+COS_MIN = 0.999       # vs the reference arithmetic (north star)
+MAX_ABS = 2e-2        # vs the reference arithmetic (north star)
+COS_SLACK = 1e-4      # ours vs f64 may trail the reference arithmetic vs f64 by this
+REL_L2_SLACK = 1e-3
+
+
+def _case(oracle, name):
+    P, G = oracle.Problem, oracle.GenSpec
+    cases = {
+        "c1": oracle.config(1, seed=11),
+        "d128_tail200": (P(1, 3, 200, 128), G(k_off_std=2.0, seed=3)),
+        "d64_t3001": (P(1, 2, 3001, 64), G(k_off_std=3.0, outlier_channels=2, outlier_scale=6.0, seed=21)),
+        "d128_gqa": (P(2, 8, 300, 128, kv_heads=2), G(k_off_std=2.0, seed=4)),
+        "d64_nosmooth": (P(2, 3, 211, 64, smooth_k=False, smooth_v=False), G(k_off_std=2.0, seed=5)),
+        "d128_causal_f16": (P(1, 4, 517, 128, dtype=1, causal=True), G(k_off_std=2.0, seed=6)),
+        "d64_causal_gqa": (P(1, 6, 333, 64, kv_heads=3, causal=True), G(k_off_std=1.0, seed=7)),
+        "n1": (P(1, 2, 1, 64), G(seed=8)),
+        "n65": (P(1, 2, 65, 128), G(seed=9)),
+        "tokens_x10": (P(1, 3, 700, 64, dtype=1), G(k_off_std=3.0, token_frac=0.02, token_scale=10.0, seed=10)),
+        "outlier_ch20": (P(1, 2, 1000, 128, dtype=1, causal=True),
+                         G(k_off_std=2.0, outlier_channels=4, outlier_scale=20.0, seed=12)),
+    }
+    return cases[name]
+
+
+SMALL = ["c1", "d128_tail200", "d64_t3001", "d128_gqa", "d64_nosmooth", "d128_causal_f16", "d64_causal_gqa",
+         "n1", "n65", "tokens_x10", "outlier_ch20"]
+
+
+def _check_attention(oracle, p, pro_oracle, o_gpu, rows, q, k, v, label):
+    emu, emu16 = oracle.sage_emulate(p, pro_oracle, rows=rows, out_dtype=p.dtype)
+    ours = oracle.decode16(gather_rows(o_gpu, rows), p.dtype)
+    ref = oracle.decode16(emu16, p.dtype)
+    e = oracle.errors(ours, ref)
+    exact = oracle.attention_f64(p, q, k, v, rows=rows)
+    e64 = oracle.errors(ours, exact)
+    emu64 = oracle.errors(ref, exact)
+    print(f"{label}: vs reference arithmetic {e}; vs f64 {e64}; reference arithmetic vs f64 {emu64}")
+    assert np.isfinite(ours).all()
+    assert e["cos"] >= COS_MIN and e["max_abs"] <= MAX_ABS, e
+    assert e64["cos"] >= emu64["cos"] - COS_SLACK, (e64, emu64)
+    assert e64["rel_l2"] <= emu64["rel_l2"] * 1.02 + REL_L2_SLACK, (e64, emu64)
+
+
+@pytest.mark.parametrize("name", SMALL)
+def test_small_cases(oracle, torch_gpu, name):
+    p, g = _case(oracle, name)
+    q, k, v = oracle.generate(p, g)
+    pro, o = run(torch_gpu, p, q, k, v)
+    want = oracle.prologue(p, q, k, v)
+    assert_prologue_equal(pro, want)
+    rows = sample_rows(p.tokens, 512)
+    _check_attention(oracle, p, want, o, rows, q, k, v, name)
+
+
+@pytest.mark.parametrize("layout", ["packed", "bhtd"])
+def test_strided_layouts(oracle, torch_gpu, layout):
+    p, g = oracle.Problem(2, 3, 389, 64), oracle.GenSpec(k_off_std=2.0, seed=13)
+    q, k, v = oracle.generate(p, g)
+    pro, o = run(torch_gpu, p, q, k, v, q_layout=layout, out_layout="bhtd" if layout == "bhtd" else "bthd")
+    _, o_ref = run(torch_gpu, p, q, k, v, want_ws=False)
+    assert_prologue_equal(pro, oracle.prologue(p, q, k, v))
+    assert np.array_equal(o, o_ref)
+
+
+def test_fp16_output_from_bf16_inputs(oracle, torch_gpu):
+    p, g = oracle.Problem(1, 2, 300, 128), oracle.GenSpec(seed=14)
+    q, k, v = oracle.generate(p, g)
+    _, o = run(torch_gpu, p, q, k, v, out_dtype=1)
+    pro = oracle.prologue(p, q, k, v)
+    rows = sample_rows(p.tokens, 300)
+    _, emu16 = oracle.sage_emulate(p, pro, rows=rows, out_dtype=1)
+    e = oracle.errors(oracle.decode16(gather_rows(o, rows), 1), oracle.decode16(emu16, 1))
+    assert e["cos"] >= COS_MIN and e["max_abs"] <= MAX_ABS, e
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_baseline_configs(oracle, torch_gpu, cfg):
+    """BASELINE.json configs at full size: prologue bit-exact over every
+    element; attention on sampled rows of every (batch, head)."""
+    p, g = oracle.config(cfg, seed=100 + cfg)
+    q, k, v = oracle.generate(p, g)
+    pro, o = run(torch_gpu, p, q, k, v)
+    want = oracle.prologue(p, q, k, v)
+    assert_prologue_equal(pro, want)
+    rows = sample_rows(p.tokens, 256 if cfg == 1 else 64, seed=cfg)
+    _check_attention(oracle, p, want, o, rows, q, k, v, f"config {cfg}")
+
+
+def test_constant_channels_come_out_exactly(oracle, torch_gpu):
+    """Size-independent property at the headline shape: a V channel that is
+    constant over tokens is removed by V smoothing (codes 0) and added back
+    as its mean, so the output equals it exactly."""
+    p, g = oracle.config(2, seed=7)
+    q, k, v = oracle.generate(p, g)
+    c = oracle.encode16(np.array([1.5, -0.375], np.float32), 0)
+    v[..., 5] = c[0]
+    v[..., 77] = c[1]
+    _, o = run(torch_gpu, p, q, k, v, want_ws=False)
+    assert (o[..., 5] == c[0]).all() and (o[..., 77] == c[1]).all()
