@@ -122,6 +122,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-peak", action="store_true", help="skip the MFMA peak probes")
+    ap.add_argument("--only", choices=["attend", "prepare"],
+                    help="profiling mode: run only this kernel group --steps times and print its timing")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box here has one GPU); "
@@ -147,6 +149,16 @@ def main() -> int:
     def step():
         sa.prepare(ws, qt, kt, vt, opts)
         sa.attend(ws, ot)
+
+    if args.only:
+        fn = (lambda: sa.attend(ws, ot)) if args.only == "attend" else (lambda: sa.prepare(ws, qt, kt, vt, opts))
+        sa.prepare(ws, qt, kt, vt, opts)
+        for _ in range(args.warmup):
+            fn()
+        ms = time_events(torch, stream, fn, args.steps)
+        print(json.dumps({"only": args.only, "config": NAMES[args.config], "ms": round(ms, 4),
+                          "tops": round(ops / (ms * 1e-3) / 1e12, 2) if args.only == "attend" else None}), flush=True)
+        return 0
 
     for _ in range(args.warmup):
         step()

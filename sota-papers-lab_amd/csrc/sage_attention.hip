@@ -21,10 +21,12 @@
 //   operand, stored by the prologue with its keys in that register order
 //   (v8_position). P never goes through LDS, and the O^T accumulator again
 //   holds one query per lane, so rescaling by alpha is lane-local.
-// - The INT8 accumulators start from the bits of 1.5 * 2^23, so each holds the
-//   float 1.5 * 2^23 + S exactly (|S| < 2^22 for D <= 128): the row max runs on
-//   the integer bits and the exp2 argument is one FMA, with the offset folded
-//   into the per-block constant (the reference's SG_FAST_EXP).
+// - The row max runs on the int32 scores (v_max3_i32); each score is then
+//   converted exactly and scaled by q_scale * k_scale inside the exp2 FMA.
+//   (Folding a 1.5 * 2^23 accumulator bias into the FMA constant, as the
+//   reference's SG_FAST_EXP does, costs ~0.75 * sc log2 units of rounding per
+//   block, which reaches 1% at the scales of outlier-heavy inputs.)
+// - O is rescaled only in blocks where some row's running max moved.
 // - O accumulates on the MFMA in fp32 across blocks (O = alpha * O + P.V):
 //   the MFMA adds its product to C exactly in fp32, so the reference's
 //   separate per-block fp32 partial is not needed.
@@ -37,19 +39,30 @@
 namespace sage {
 
 constexpr int ATTN_BN = 64;  // keys per iteration (one K scale, one V block)
-constexpr unsigned NEG_INF_BITS = 0xff800000u;
-// Largest q_scale * k_scale for which the biased-accumulator shortcut is used:
-// the offset -1.5 * 2^23 * sc folded into the exp2 argument rounds by up to
-// about 0.75 * sc in log2 units, so above this the wave converts S exactly.
-constexpr float FAST_SC_MAX = 2.0e-4f;
+// A row's reference point m moves when a block's max exceeds it by more than
+// RESCALE_SLACK (log2 units), and P = 2^(x - m + RESCALE_TARGET) <= 448, the
+// E4M3 maximum. With slack 0 this is the reference's running max, under which
+// the row's largest score maps to exactly 448 (an E4M3 value, so the dominant
+// key carries no rounding error); a positive slack would skip more rescales
+// but rounds that key by up to 6%, which the normalisation by the unrounded
+// row sum does not cancel. O is rescaled only in blocks where some row's
+// max moved, which is exact.
+constexpr float RESCALE_SLACK = 0.0f;
+constexpr float RESCALE_TARGET = 8.807354922057604f;  // log2(448) - RESCALE_SLACK
 
-// Two K/V stages as separate LDS objects: the compiler then knows that the
-// direct-to-LDS prefetch into one never aliases the MFMA operand reads of the
-// other, and lets them overlap.
-template <int D>
-struct Stages {
-    static constexpr int TILE = ATTN_BN * D;  // bytes of one K tile and of one V tile
-};
+// Value of lane ^ 32 (the other half of the wave) with one v_permlane32_swap.
+// The swap returns both operands' new values; in each half of the wave one of
+// the two holds the partner's value. `first` (from half_selector) says which.
+__device__ __forceinline__ int swap_halves(int x, bool first) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return first ? (int)r[0] : (int)r[1];
+}
+__device__ __forceinline__ float swap_halves(float x, bool first) {
+    return __int_as_float(swap_halves(__float_as_int(x), first));
+}
+__device__ __forceinline__ bool half_selector(int lane) {
+    return (int)__builtin_amdgcn_permlane32_swap(lane, lane, false, false)[0] != lane;
+}
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q8, const float* __restrict__ q_scale,
@@ -60,13 +73,19 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
     constexpr int BN = ATTN_BN;
     constexpr int KS = D / 32;            // INT8 k-steps of 32 channels
     constexpr int DT = D / 32;            // 32-channel tiles of O^T
-    constexpr int TILE = Stages<D>::TILE; // bytes of one K tile and of one V tile
+    constexpr int TILE = BN * D;          // bytes of one K tile and of one V tile
     constexpr int CPT = TILE / 16 / 256;  // 16-byte chunks per thread per tile
     constexpr int KCPR = D / 16;          // chunks per K row
     static_assert(CPT >= 1, "tile too small for 256 threads");
 
-    __shared__ __attribute__((aligned(16))) uint8_t lds0[2 * TILE];
-    __shared__ __attribute__((aligned(16))) uint8_t lds1[2 * TILE];
+    // K and V are double-buffered separately: step j reads K(j+1) and V(j)
+    // while K(j+2) and V(j+1) arrive, so both rings have period two. Separate
+    // LDS objects let the compiler see that the direct-to-LDS prefetch into
+    // one buffer never aliases the MFMA operand reads of another.
+    __shared__ __attribute__((aligned(16))) uint8_t ldsK0[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsK1[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsV0[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsV1[TILE];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 31, half = lane >> 5;
     const int qt = CAUSAL ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;  // heavy tiles first
@@ -74,6 +93,7 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
     const long long bh = (long long)b * g.heads + h, bhk = (long long)b * g.kv_heads + hk;
     const int q0 = qt * ATTN_ROWS + wave * 32;  // first query of this wave
     const int qi = q0 + col;                    // this lane's query
+    const bool sel = half_selector(lane);
 
     // Q^T operand: lane holds channels 32s + 16*half .. +15 of its query.
     v4i qa[KS];
@@ -92,21 +112,55 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
 
     int nblk = g.kblocks;
     if (CAUSAL) nblk = min(nblk, (qt * ATTN_ROWS + ATTN_ROWS - 1) / BN + 1);
+    // Leading blocks no query of the workgroup needs masked: every key exists
+    // and (causal) precedes the workgroup's first query.
+    int nfull = min(nblk, g.tk / BN);
+    if (CAUSAL) nfull = min(nfull, (qt * ATTN_ROWS + 1) / BN);
 
     const uint8_t* kg = reinterpret_cast<const uint8_t*>(k8) + bhk * (long long)g.tk_pad * D;
     const uint8_t* vg = v8 + bhk * (long long)g.tk_pad * D;
     const float* ksc = k_scale + bhk * g.kblocks;
 
-    // Direct global -> LDS copy of one block's K and V tiles into `dst`. Lane
-    // `lane` of wave `wave` fills physical chunk c of the tile, so it fetches
-    // the logical chunk that the swizzle puts there (swz is an involution).
-    auto fetch = [&](int blk, uint8_t* dst) {
+    // Direct global -> LDS copy of one tile. Lane `lane` of wave `wave` fills
+    // physical chunk c of the tile, so it fetches the logical chunk that the
+    // swizzle puts there (swz is an involution).
+    auto fetch = [&](const uint8_t* src_base, int blk, uint8_t* dst) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < CPT; i++) {
             const int c0 = i * 256 + wave * 64;
-            const long long src = (long long)blk * TILE + 16 * swz(c0 + lane);
-            __builtin_amdgcn_global_load_lds(kg + src, (__attribute__((address_space(3))) void*)(dst + 16 * c0), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(vg + src, (__attribute__((address_space(3))) void*)(dst + TILE + 16 * c0), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(src_base + (long long)blk * TILE + 16 * swz(c0 + lane),
+                                             (__attribute__((address_space(3))) void*)(dst + 16 * c0), 16, 0, 0);
+        }
+    };
+
+    // Per-lane LDS byte offsets of the MFMA operands. K row 32t + col, chunk
+    // 2ks + half sits at swz((32t + col) * KCPR + 2ks + half); since
+    // (32t + col) * KCPR is a multiple of 8 whose line index differs from
+    // col's by a multiple of 8 only through t, the sub-tile term 32t * KCPR
+    // is a constant offset and only the KS chunk columns need registers. V^T
+    // row 32dt + col likewise differs from row col by a whole number of lines.
+    int koff[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) koff[ks] = 16 * swz(col * KCPR + 2 * ks + half);
+    const int voff0 = 16 * swz(col * 4 + 2 * half), voff1 = 16 * swz(col * 4 + 2 * half + 1);
+
+    // S^T of one block (keys 32t .. 32t + 31 in s[t]) from the K tile `kt`.
+    auto qk = [&](const uint8_t* kt, v16i (&s)[2]) __attribute__((always_inline)) {
+        uint4 ka[2][KS];
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++)
+                ka[t][ks] = *reinterpret_cast<const uint4*>(kt + 16 * 32 * t * KCPR + koff[ks]);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) s[t][r] = 0;
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+                const v4i av = {(int)ka[t][ks].x, (int)ka[t][ks].y, (int)ka[t][ks].z, (int)ka[t][ks].w};
+                s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qa[ks], s[t], 0, 0, 0);
+            }
         }
     };
 
@@ -115,87 +169,80 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[dt][r] = 0.f;
+    // m: the running reference point of the row (log2 units); P = 2^(x - m + target).
     float m = -1.0e30f, l = 0.f;
-    const float kMagic = 12582912.0f;          // 1.5 * 2^23
-    const float kLog448 = 8.807354922057604f;  // log2(448): P fills the E4M3 range
+    const float kTarget = RESCALE_TARGET;
 
-    // One 64-key block whose K and V tiles are in `cur`; prefetches block
-    // blk + 1 into `nxt` first.
-    auto step = [&](int blk, const uint8_t* cur, uint8_t* nxt) {
-        if (blk + 1 < nblk) fetch(blk + 1, nxt);
-        const uint4* lk = reinterpret_cast<const uint4*>(cur);
-        const uint4* lv = reinterpret_cast<const uint4*>(cur + TILE);
-        const float sc = qs * ksc[blk];
-        const bool fast = __all(sc < FAST_SC_MAX);
+    v16i S0[2], S1[2];
 
-        // S^T for keys 32t .. 32t + 31 of the block; with `fast` the
-        // accumulators start at the bits of 1.5 * 2^23 and then hold the
-        // float 1.5 * 2^23 + S exactly.
-        v16i s[2];
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) s[t][r] = fast ? 0x4b400000 : 0;
-#pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const uint4 a = lk[swz((32 * t + col) * KCPR + 2 * ks + half)];
-                const v4i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w};
-                s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qa[ks], s[t], 0, 0, 0);
-            }
+    // Step j: prefetch K(j+2) and V(j+1), issue the QK^T MFMAs of block j+1
+    // (they run while this wave does the softmax of block j), then P.V of
+    // block j. PAR = j % 2 picks the buffers and the S registers.
+    // k_fill held K(j) and gets K(j+2); k_next holds K(j+1); v_cur holds V(j);
+    // v_fill held V(j-1) and gets V(j+1). sc: S(j), sn: S(j+1).
+    auto step = [&](int blk, uint8_t* k_fill, const uint8_t* k_next, const uint8_t* v_cur, uint8_t* v_fill,
+                    v16i (&sc)[2], v16i (&sn)[2]) __attribute__((always_inline)) {
+        // Workgroup-uniform: does any key of this block need masking?
+        const bool MASK = blk >= nfull;
+        if (blk + 2 < nblk) fetch(kg, blk + 2, k_fill);
+        if (blk + 1 < nblk) {
+            fetch(vg, blk + 1, v_fill);
+            qk(k_next, sn);
         }
-
-        // Keys past the sequence, and keys after the query when causal.
-        const bool mask = (blk + 1) * BN > g.tk || (CAUSAL && blk * BN + BN - 1 > q0);
-        const int masked = fast ? (int)NEG_INF_BITS : INT_MIN;
-        if (mask) {
+        // Phase fences: keep the scheduler from hoisting the next phase's loads
+        // into this one (which would push the register count past 256).
+        __builtin_amdgcn_sched_barrier(0);
+        // q_scale * k_scale, kept above zero so that -inf * scl stays -inf.
+        const float scl = fmaxf(qs * ksc[blk], 1.0e-30f);
+        if (MASK) {
+            // Keys past the sequence, and keys after the query when causal. Element
+            // (t, r) is key blk*BN + 4*half + c with the constant c below, so one
+            // per-lane limit decides every element.
+            int lim = g.tk - blk * BN - 4 * half;
+            if (CAUSAL) lim = min(lim, qi - blk * BN - 4 * half + 1);
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int key = blk * BN + 32 * t + 8 * (r >> 2) + 4 * half + (r & 3);
-                    if (key >= g.tk || (CAUSAL && key > qi)) s[t][r] = masked;
-                }
+                for (int r = 0; r < 16; r++)
+                    if (32 * t + 8 * (r >> 2) + (r & 3) >= lim) sc[t][r] = INT_MIN;
         }
-        int mx = s[0][0];
+        // Row max over this lane's 32 keys, three at a time (v_max3), then the partner half.
+        int mx = max(sc[0][0], sc[1][15]);
+#pragma unroll
+        for (int i = 1; i < 31; i += 2) mx = max(max(mx, sc[i >> 4][i & 15]), sc[(i + 1) >> 4][(i + 1) & 15]);
+        mx = max(mx, swap_halves(mx, sel));
+
+        // The block max in log2 units; the reference point moves only when the
+        // block exceeds it by more than RESCALE_SLACK (then O and l are rescaled).
+        const float mblk = mx == INT_MIN ? -INFINITY : (float)mx * scl;
+        const bool grow = mblk > m + RESCALE_SLACK;
+        const float mnew = grow ? mblk : m;
+        const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+        m = mnew;
+
+        // Scores as floats; a masked one becomes -inf, so (scl > 0) its exp2 is 0.
+        float p[2][16];
+        if (MASK) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) p[t][r] = sc[t][r] == INT_MIN ? -INFINITY : (float)sc[t][r];
+        } else {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) p[t][r] = (float)sc[t][r];
+        }
+        const float off = kTarget - mnew;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) mx = max(mx, s[t][r]);
-        mx = max(mx, __shfl_xor(mx, 32, 64));
-
-        float p[2][16];
-        float sum = 0.f, alpha;
-        if (fast) {
-            const float negms = -kMagic * sc;
-            const float mnew = fmaxf(m, fmaf(__int_as_float(mx), sc, negms));
-            alpha = __builtin_amdgcn_exp2f(m - mnew);
-            m = mnew;
-            const float off = (kLog448 - mnew) + negms;
+            for (int r = 0; r < 16; r++) p[t][r] = __builtin_amdgcn_exp2f(fmaf(p[t][r], scl, off));
+        float sum = 0.f;
 #pragma unroll
-            for (int t = 0; t < 2; t++)
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    float e = __builtin_amdgcn_exp2f(fmaf(__int_as_float(s[t][r]), sc, off));
-                    if (mask && s[t][r] == masked) e = 0.f;
-                    p[t][r] = e;
-                    sum += e;
-                }
-        } else {
-            const float mblk = mx == INT_MIN ? -INFINITY : (float)mx * sc;
-            const float mnew = fmaxf(m, mblk);
-            alpha = __builtin_amdgcn_exp2f(m - mnew);
-            m = mnew;
-            const float off = kLog448 - mnew;
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    float e = __builtin_amdgcn_exp2f(fmaf((float)s[t][r], sc, off));
-                    if (mask && s[t][r] == masked) e = 0.f;
-                    p[t][r] = e;
-                    sum += e;
-                }
-        }
+            for (int r = 0; r < 16; r++) sum += p[t][r];
         l = fmaf(l, alpha, sum);
 
         // P^T operand: register j holds keys of accumulators 4(j%4)..+3 of sub-tile j/4.
@@ -206,8 +253,15 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
             const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0], p[t][r0 + 1], 0, false);
             pb[j] = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0 + 2], p[t][r0 + 3], lo, true);
         }
-
-        if (__any(alpha != 1.0f)) {
+        __builtin_amdgcn_sched_barrier(0);
+        // V^T operands of block j (row = channel, 4 chunks per 64-byte row).
+        uint4 va[DT][2];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            va[dt][0] = *reinterpret_cast<const uint4*>(v_cur + 16 * 128 * dt + voff0);
+            va[dt][1] = *reinterpret_cast<const uint4*>(v_cur + 16 * 128 * dt + voff1);
+        }
+        if (__any(grow)) {
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
@@ -215,24 +269,29 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
         }
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
-            const int u = (32 * dt + col) * 4 + 2 * half;  // V^T row = channel, 4 chunks per row
-            const uint4 a0 = lv[swz(u)], a1 = lv[swz(u + 1)];
-            const v8i av = {(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+            const v8i av = {(int)va[dt][0].x, (int)va[dt][0].y, (int)va[dt][0].z, (int)va[dt][0].w,
+                            (int)va[dt][1].x, (int)va[dt][1].y, (int)va[dt][1].z, (int)va[dt][1].w};
             o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, pb, o[dt], 0, 0, 0, 127, 0, 127);
         }
-        // Drains this wave's prefetch and publishes it; nobody reads `cur` after.
+        // Drains this wave's prefetches and publishes them; the buffers read
+        // in this step are free afterwards.
         __syncthreads();
     };
 
-    fetch(0, lds0);
+    fetch(kg, 0, ldsK0);
+    fetch(vg, 0, ldsV0);
+    if (nblk > 1) fetch(kg, 1, ldsK1);
     __syncthreads();
+    qk(ldsK0, S0);
+    __syncthreads();  // every wave has read K(0) before step 0 refills its buffer
+
     for (int blk = 0; blk < nblk; blk += 2) {
-        step(blk, lds0, lds1);
-        if (blk + 1 < nblk) step(blk + 1, lds1, lds0);
+        step(blk, ldsK0, ldsK1, ldsV0, ldsV1, S0, S1);
+        if (blk + 1 < nblk) step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0, S1, S0);
     }
 
     // out = O / l * v_scale + v_mean; lane holds channels 32dt + 8j + 4*half + 0..3.
-    const float lt = l + __shfl_xor(l, 32, 64);
+    const float lt = l + swap_halves(l, sel);
     const float inv = 1.0f / lt;
     if (qi < g.tokens) {
         const float* vmean = stats + bhk * 4 * D + D;
