@@ -88,7 +88,7 @@ def lib() -> C.CDLL:
         l.oracle_prologue.argtypes = [C.POINTER(_Problem), vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int]
         l.oracle_attention_f64.argtypes = [C.POINTER(_Problem), C.c_int, C.c_float, vp, vp, vp, vp, C.c_int, vp, C.c_int]
         l.oracle_sage_emulate.argtypes = [C.POINTER(_Problem), C.c_int, vp, vp, vp, vp, vp, vp, vp, C.c_int, vp, vp,
-                                          C.c_int, C.c_int]
+                                          C.c_int, C.c_int, C.c_int]
         l.oracle_errors.argtypes = [vp, vp, C.c_size_t, vp]
         _lib = l
     return _lib
@@ -261,15 +261,17 @@ def attention_f64(p: Problem, q, k, v, rows=None, threads: int = 0) -> np.ndarra
     return out
 
 
-def sage_emulate(p: Problem, pro: dict, rows=None, out_dtype: int = BF16, threads: int = 0):
+def sage_emulate(p: Problem, pro: dict, rows=None, out_dtype: int = BF16, threads: int = 0, fast_exp: bool = True):
     """The reference's quantised attention arithmetic on `pro`; returns
-    (float32 [B,H,R,D] before 16-bit rounding, uint16 codes of out_dtype)."""
+    (float32 [B,H,R,D] before 16-bit rounding, uint16 codes of out_dtype).
+    fast_exp=True is the reference's default logit arithmetic (SG_FAST_EXP=1,
+    sage_attn.cu:59-61); False converts the scores exactly (SG_FAST_EXP=0)."""
     r, R = _rows(rows, p.tokens)
     out = np.empty((p.batch, p.heads, R, p.head_dim), np.float32)
     o16 = np.empty(out.shape, np.uint16)
     lib().oracle_sage_emulate(C.byref(p._c()), int(p.causal), _p(pro["q8"]), _p(pro["q_scale"]), _p(pro["k8"]),
                               _p(pro["k_scale"]), _p(pro["v8"]), _p(pro["stats"]), None if r is None else _p(r), R,
-                              _p(out), _p(o16), out_dtype, threads)
+                              _p(out), _p(o16), out_dtype, int(bool(fast_exp)), threads)
     return out, o16
 
 

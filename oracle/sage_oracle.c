@@ -461,9 +461,15 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
 static inline float ex2f_cr(float x) { return (float)exp2((double)x); }
 
 /* The reference's attention arithmetic on quantised tensors
- * (sage_attn.cu:262-344 with SG_FAST_EXP=0, :402-421):
- *   x = S (exact int32), mnew = max(m, fmaf(max S, sc, 0)), sc = qs*ks;
- *   alpha = 2^(m - mnew); off = log2(448) - mnew; p = 2^fmaf(S, sc, off);
+ * (sage_attn.cu:262-344, :402-421), sc = qs*ks:
+ *   SG_FAST_EXP=0 (fast_exp = 0): x = S (exact int32 as float),
+ *     xoff = 0;
+ *   SG_FAST_EXP=1 (fast_exp = 1, the reference's default, sage_attn.cu:59-61):
+ *     x = 1.5*2^23 + S (the float whose bits are 0x4B400000 + S, exact for
+ *     |S| < 2^22; sage_attn.cu:23-25,265-270), xoff = -(1.5*2^23) * sc in
+ *     fp32 (sage_attn.cu:284);
+ *   then mnew = max(m, fmaf(max x, sc, xoff)); alpha = 2^(m - mnew);
+ *   off = (log2(448) - mnew) + xoff; p = 2^fmaf(x, sc, off);
  *   l = fmaf(l, alpha, sum p); P8 = e4m3(p); PV = sum P8*V8 per 64 keys (fp32,
  *   accumulated exactly here); O = fmaf(O, alpha, PV);
  *   out = fmaf(O * (1/l), v_scale, v_mean).
@@ -473,8 +479,10 @@ static inline float ex2f_cr(float x) { return (float)exp2((double)x); }
  * within the quantisation error; sequential sums replace the GPU's lane order. */
 void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, const float* q_scale,
                          const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* stats,
-                         const int* rows, int nrows, float* out, uint16_t* out16, int out_dtype, int threads) {
+                         const int* rows, int nrows, float* out, uint16_t* out16, int out_dtype, int fast_exp,
+                         int threads) {
     const int B = p->batch, H = p->heads, HK = p->kv_heads, N = p->tokens, D = p->head_dim, G = H / HK;
+    const float kMagic = 12582912.0f; /* 1.5 * 2^23 */
     const size_t tq_pad = round_up((size_t)N, ORACLE_QTILE), tk_pad = round_up((size_t)N, ORACLE_KBLOCK);
     const int nblk = (int)(tk_pad / ORACLE_KBLOCK);
     const int R = rows ? nrows : N;
@@ -516,14 +524,17 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
                         }
                         S[r] = ok ? s : INT32_MIN;
                     }
+                    /* x as the reference holds it: exact, or biased by kMagic (both exact floats) */
+                    const float bias = fast_exp ? kMagic : 0.f;
+                    const float xoff = fast_exp ? -kMagic * sc : 0.f;
                     float mnew = m;
-                    if (have) mnew = fmaxf(m, fmaf((float)smax, sc, 0.f));
+                    if (have) mnew = fmaxf(m, fmaf(bias + (float)smax, sc, xoff));
                     const float alpha = ex2f_cr(m - mnew);
                     m = mnew;
-                    const float off = kLog448 - mnew;
+                    const float off = (kLog448 - mnew) + xoff;
                     float sum = 0.f;
                     for (int r = 0; r < ORACLE_KBLOCK; r++) {
-                        float pr = S[r] == INT32_MIN ? 0.f : ex2f_cr(fmaf((float)S[r], sc, off));
+                        float pr = S[r] == INT32_MIN ? 0.f : ex2f_cr(fmaf(bias + (float)S[r], sc, off));
                         P[r] = pr;
                         sum += pr;
                     }

@@ -116,11 +116,14 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
  * online softmax in log2 units with a correctly rounded exp2, P -> E4M3,
  * per-64-key fp32 P.V partial folded as O = O*alpha + PV, then
  * out = O/l * v_scale + v_mean. `out` is fp32 before the final 16-bit
- * rounding; `out16` (may be NULL) receives it rounded to `out_dtype`. */
+ * rounding; `out16` (may be NULL) receives it rounded to `out_dtype`.
+ * fast_exp = 1 is the reference's default logit arithmetic (SG_FAST_EXP=1:
+ * scores biased by 1.5 * 2^23, the bias removed inside the exp2 FMA);
+ * fast_exp = 0 converts the int32 scores exactly (SG_FAST_EXP=0). */
 void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, const float* q_scale,
                          const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* stats,
                          const int* rows, int nrows, float* out, uint16_t* out16, int out_dtype,
-                         int threads);
+                         int fast_exp, int threads);
 
 /* Errors of `ours` against `ref` (reference.rs:202-225):
  * out[0] cos, [1] rel_l1, [2] rel_l2, [3] max_abs, [4] ref_max. */

@@ -21,11 +21,13 @@
 //   operand, stored by the prologue with its keys in that register order
 //   (v8_position). P never goes through LDS, and the O^T accumulator again
 //   holds one query per lane, so rescaling by alpha is lane-local.
-// - The row max runs on the int32 scores (v_max3_i32); each score is then
-//   converted exactly and scaled by q_scale * k_scale inside the exp2 FMA.
-//   (Folding a 1.5 * 2^23 accumulator bias into the FMA constant, as the
-//   reference's SG_FAST_EXP does, costs ~0.75 * sc log2 units of rounding per
-//   block, which reaches 1% at the scales of outlier-heavy inputs.)
+// - The INT8 accumulators start from the bits of 1.5 * 2^23, so each score
+//   register already holds the float 1.5 * 2^23 + S (exact for |S| < 2^22):
+//   no int -> float conversions. The row max runs on those bits (positive
+//   floats order like their bit patterns, v_max3_i32), and the bias comes
+//   off inside the exp2 FMA through xoff = -(1.5 * 2^23) * sc, the
+//   reference's default logit arithmetic (SG_FAST_EXP=1, sage_attn.cu:23-31,
+//   262-300), in the same fp32 operation order.
 // - O is rescaled only in blocks where some row's running max moved.
 // - O accumulates on the MFMA in fp32 across blocks (O = alpha * O + P.V):
 //   the MFMA adds its product to C exactly in fp32, so the reference's
@@ -39,6 +41,9 @@
 namespace sage {
 
 constexpr int ATTN_BN = 64;  // keys per iteration (one K scale, one V block)
+constexpr int MAGIC_BITS = 0x4B400000;      // bits of 1.5 * 2^23
+constexpr float MAGIC = 12582912.0f;        // 1.5 * 2^23
+constexpr int NEG_INF_BITS = (int)0xFF800000;  // -inf: below every biased score as an int
 // A row's reference point m moves when a block's max exceeds it by more than
 // RESCALE_SLACK (log2 units), and P = 2^(x - m + RESCALE_TARGET) <= 448, the
 // E4M3 maximum. With slack 0 this is the reference's running max, under which
@@ -124,27 +129,31 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
     // Direct global -> LDS copy of one tile. Lane `lane` of wave `wave` fills
     // physical chunk c of the tile, so it fetches the logical chunk that the
     // swizzle puts there (swz is an involution).
-    auto fetch = [&](const uint8_t* src_base, int blk, uint8_t* dst) __attribute__((always_inline)) {
+    auto fetch = [&](const uint8_t* src_base, int blk, uint8_t* dst, int cpr) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < CPT; i++) {
             const int c0 = i * 256 + wave * 64;
-            __builtin_amdgcn_global_load_lds(src_base + (long long)blk * TILE + 16 * swz(c0 + lane),
+            __builtin_amdgcn_global_load_lds(src_base + (long long)blk * TILE + 16 * swz(c0 + lane, cpr),
                                              (__attribute__((address_space(3))) void*)(dst + 16 * c0), 16, 0, 0);
         }
     };
 
     // Per-lane LDS byte offsets of the MFMA operands. K row 32t + col, chunk
-    // 2ks + half sits at swz((32t + col) * KCPR + 2ks + half); since
-    // (32t + col) * KCPR is a multiple of 8 whose line index differs from
-    // col's by a multiple of 8 only through t, the sub-tile term 32t * KCPR
-    // is a constant offset and only the KS chunk columns need registers. V^T
-    // row 32dt + col likewise differs from row col by a whole number of lines.
+    // 2ks + half sits at swz((32t + col) * KCPR + 2ks + half); 32t rows are a
+    // whole number of 256-byte lines whose count is a multiple of KCPR, so
+    // the XOR term does not depend on t: the sub-tile term 32t * KCPR is a
+    // constant offset and only the KS chunk columns need registers. V^T row
+    // 32dt + col (4 chunks a row) likewise shares row col's XOR term.
     int koff[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) koff[ks] = 16 * swz(col * KCPR + 2 * ks + half);
-    const int voff0 = 16 * swz(col * 4 + 2 * half), voff1 = 16 * swz(col * 4 + 2 * half + 1);
+    for (int ks = 0; ks < KS; ks++) koff[ks] = 16 * swz(col * KCPR + 2 * ks + half, KCPR);
+    const int voff0 = 16 * swz(col * 4 + 2 * half, 4), voff1 = 16 * swz(col * 4 + 2 * half + 1, 4);
 
-    // S^T of one block (keys 32t .. 32t + 31 in s[t]) from the K tile `kt`.
+    // S^T of one block (keys 32t .. 32t + 31 in s[t]) from the K tile `kt`,
+    // each accumulator starting from the 1.5 * 2^23 bias.
+    v16i magic;
+#pragma unroll
+    for (int r = 0; r < 16; r++) magic[r] = MAGIC_BITS;
     auto qk = [&](const uint8_t* kt, v16i (&s)[2]) __attribute__((always_inline)) {
         uint4 ka[2][KS];
 #pragma unroll
@@ -155,11 +164,9 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
 #pragma unroll
         for (int t = 0; t < 2; t++) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) s[t][r] = 0;
-#pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 const v4i av = {(int)ka[t][ks].x, (int)ka[t][ks].y, (int)ka[t][ks].z, (int)ka[t][ks].w};
-                s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qa[ks], s[t], 0, 0, 0);
+                s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qa[ks], ks ? s[t] : magic, 0, 0, 0);
             }
         }
     };
@@ -182,11 +189,13 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
     // v_fill held V(j-1) and gets V(j+1). sc: S(j), sn: S(j+1).
     auto step = [&](int blk, uint8_t* k_fill, const uint8_t* k_next, const uint8_t* v_cur, uint8_t* v_fill,
                     v16i (&sc)[2], v16i (&sn)[2]) __attribute__((always_inline)) {
+        // The reference's fp32 operation order for the logits: no FMA contraction.
+#pragma clang fp contract(off)
         // Workgroup-uniform: does any key of this block need masking?
         const bool MASK = blk >= nfull;
-        if (blk + 2 < nblk) fetch(kg, blk + 2, k_fill);
+        if (blk + 2 < nblk) fetch(kg, blk + 2, k_fill, KCPR);
         if (blk + 1 < nblk) {
-            fetch(vg, blk + 1, v_fill);
+            fetch(vg, blk + 1, v_fill, 4);
             qk(k_next, sn);
         }
         // Phase fences: keep the scheduler from hoisting the next phase's loads
@@ -194,6 +203,7 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
         __builtin_amdgcn_sched_barrier(0);
         // q_scale * k_scale, kept above zero so that -inf * scl stays -inf.
         const float scl = fmaxf(qs * ksc[blk], 1.0e-30f);
+        const float xoff = -MAGIC * scl;
         if (MASK) {
             // Keys past the sequence, and keys after the query when causal. Element
             // (t, r) is key blk*BN + 4*half + c with the constant c below, so one
@@ -204,7 +214,7 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int r = 0; r < 16; r++)
-                    if (32 * t + 8 * (r >> 2) + (r & 3) >= lim) sc[t][r] = INT_MIN;
+                    if (32 * t + 8 * (r >> 2) + (r & 3) >= lim) sc[t][r] = NEG_INF_BITS;
         }
         // Row max over this lane's 32 keys, three at a time (v_max3), then the partner half.
         int mx = max(sc[0][0], sc[1][15]);
@@ -214,30 +224,21 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
 
         // The block max in log2 units; the reference point moves only when the
         // block exceeds it by more than RESCALE_SLACK (then O and l are rescaled).
-        const float mblk = mx == INT_MIN ? -INFINITY : (float)mx * scl;
+        // (a fully masked block gives -inf, which leaves m alone)
+        const float mblk = fmaf(__int_as_float(mx), scl, xoff);
         const bool grow = mblk > m + RESCALE_SLACK;
         const float mnew = grow ? mblk : m;
         const float alpha = __builtin_amdgcn_exp2f(m - mnew);
         m = mnew;
 
-        // Scores as floats; a masked one becomes -inf, so (scl > 0) its exp2 is 0.
+        // P = 2^(x sc + off) of the biased scores; a masked one is -inf, so
+        // (scl > 0) its exp2 is 0.
+        const float off = (kTarget - mnew) + xoff;
         float p[2][16];
-        if (MASK) {
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) p[t][r] = sc[t][r] == INT_MIN ? -INFINITY : (float)sc[t][r];
-        } else {
-#pragma unroll
-            for (int t = 0; t < 2; t++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) p[t][r] = (float)sc[t][r];
-        }
-        const float off = kTarget - mnew;
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) p[t][r] = __builtin_amdgcn_exp2f(fmaf(p[t][r], scl, off));
+            for (int r = 0; r < 16; r++) p[t][r] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sc[t][r]), scl, off));
         float sum = 0.f;
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -278,9 +279,9 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
         __syncthreads();
     };
 
-    fetch(kg, 0, ldsK0);
-    fetch(vg, 0, ldsV0);
-    if (nblk > 1) fetch(kg, 1, ldsK1);
+    fetch(kg, 0, ldsK0, KCPR);
+    fetch(vg, 0, ldsV0, 4);
+    if (nblk > 1) fetch(kg, 1, ldsK1, KCPR);
     __syncthreads();
     qk(ldsK0, S0);
     __syncthreads();  // every wave has read K(0) before step 0 refills its buffer

@@ -108,9 +108,14 @@ __host__ __device__ __forceinline__ int v8_position(int k) {
     return 32 * ((k >> 2) & 1) + 16 * (k >> 5) + 4 * ((k >> 3) & 3) + (k & 3);
 }
 
-// XOR swizzle of 16-byte chunk u inside 128-byte lines of an LDS tile: lanes
-// that read one chunk column of eight consecutive rows hit eight different
-// bank groups.
-__device__ __forceinline__ int swz(int u) { return (u & ~7) | ((u ^ (u >> 3)) & 7); }
+// XOR swizzle of 16-byte chunk u of an LDS tile whose rows are CPR chunks
+// long (CPR = 4 or 8). gfx950's LDS serves a ds_read_b128 sixteen lanes at a
+// time from 64 four-byte banks, i.e. one 256-byte line of sixteen chunks per
+// cycle. Sixteen lanes that read the same chunk column of sixteen consecutive
+// rows span 16 / CPR rows per line, so the chunk-in-row bits are XORed with
+// the line index: the sixteen reads then land in sixteen different chunk slots
+// of the line. The XOR touches only bits below the line index, so swz is an
+// involution and keeps every chunk inside its row (cpr = 4 or 8).
+__device__ __forceinline__ int swz(int u, int cpr) { return u ^ ((u >> 4) & (cpr - 1)); }
 
 }  // namespace sage
