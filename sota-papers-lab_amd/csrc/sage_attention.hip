@@ -65,6 +65,19 @@ __device__ __forceinline__ int swap_halves(int x, bool first) {
 __device__ __forceinline__ float swap_halves(float x, bool first) {
     return __int_as_float(swap_halves(__float_as_int(x), first));
 }
+// The dispatcher deals workgroups to the 8 XCDs round-robin by linear id,
+// and each XCD has its own L2. Tile t (query tile fastest, then head, then
+// batch) goes to the workgroup that gives XCD x the contiguous range of
+// tiles [x * per, (x + 1) * per): the workgroups that share a head's K and V
+// then read them through one L2 instead of eight. The last total % 8 tiles
+// keep their place.
+constexpr int NUM_XCD = 8;
+__device__ __forceinline__ int xcd_tile(int lin, int total) {
+    const int per = total / NUM_XCD;
+    if (lin >= per * NUM_XCD) return lin;
+    return (lin % NUM_XCD) * per + lin / NUM_XCD;
+}
+
 __device__ __forceinline__ bool half_selector(int lane) {
     return (int)__builtin_amdgcn_permlane32_swap(lane, lane, false, false)[0] != lane;
 }
@@ -93,8 +106,10 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
     __shared__ __attribute__((aligned(16))) uint8_t ldsV1[TILE];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 31, half = lane >> 5;
-    const int qt = CAUSAL ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;  // heavy tiles first
-    const int h = blockIdx.y, b = blockIdx.z, hk = h / g.group;
+    const int ntq = gridDim.x;
+    const int tile = xcd_tile(blockIdx.x + ntq * (blockIdx.y + gridDim.y * blockIdx.z), ntq * gridDim.y * gridDim.z);
+    const int qt = CAUSAL ? ntq - 1 - tile % ntq : tile % ntq;  // causal: heavy tiles first
+    const int h = (tile / ntq) % g.heads, b = tile / (ntq * g.heads), hk = h / g.group;
     const long long bh = (long long)b * g.heads + h, bhk = (long long)b * g.kv_heads + hk;
     const int q0 = qt * ATTN_ROWS + wave * 32;  // first query of this wave
     const int qi = q0 + col;                    // this lane's query
