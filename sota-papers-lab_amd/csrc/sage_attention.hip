@@ -44,16 +44,7 @@ constexpr int ATTN_BN = 64;  // keys per iteration (one K scale, one V block)
 constexpr int MAGIC_BITS = 0x4B400000;      // bits of 1.5 * 2^23
 constexpr float MAGIC = 12582912.0f;        // 1.5 * 2^23
 constexpr int NEG_INF_BITS = (int)0xFF800000;  // -inf: below every biased score as an int
-// A row's reference point m moves when a block's max exceeds it by more than
-// RESCALE_SLACK (log2 units), and P = 2^(x - m + RESCALE_TARGET) <= 448, the
-// E4M3 maximum. With slack 0 this is the reference's running max, under which
-// the row's largest score maps to exactly 448 (an E4M3 value, so the dominant
-// key carries no rounding error); a positive slack would skip more rescales
-// but rounds that key by up to 6%, which the normalisation by the unrounded
-// row sum does not cancel. O is rescaled only in blocks where some row's
-// max moved, which is exact.
-constexpr float RESCALE_SLACK = 0.0f;
-constexpr float RESCALE_TARGET = 8.807354922057604f;  // log2(448) - RESCALE_SLACK
+constexpr float LOG2_448 = 8.807354922057604f;  // P = 448 for the row max: E4M3's largest finite
 
 // Value of lane ^ 32 (the other half of the wave) with one v_permlane32_swap.
 // The swap returns both operands' new values; in each half of the wave one of
@@ -83,12 +74,15 @@ __device__ __forceinline__ bool half_selector(int lane) {
 }
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q8, const float* __restrict__ q_scale,
+__global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* __restrict__ q8, const float* __restrict__ q_scale,
                                                     const int8_t* __restrict__ k8,
                                                     const float* __restrict__ k_scale,
                                                     const uint8_t* __restrict__ v8, const float* __restrict__ stats,
                                                     uint16_t* __restrict__ out, Geom g) {
     constexpr int BN = ATTN_BN;
+    // Head dim 128 pipelines QK^T one block ahead (two waves a SIMD); head dim
+    // 64 fits three waves a SIMD without it.
+    constexpr bool PIPE = D == 128;
     constexpr int KS = D / 32;            // INT8 k-steps of 32 channels
     constexpr int DT = D / 32;            // 32-channel tiles of O^T
     constexpr int TILE = BN * D;          // bytes of one K tile and of one V tile
@@ -191,35 +185,18 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
     for (int dt = 0; dt < DT; dt++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[dt][r] = 0.f;
-    // m: the running reference point of the row (log2 units); P = 2^(x - m + target).
+    // m: the row's running max (log2 units); P = 2^(x - m + log2 448).
     float m = -1.0e30f, l = 0.f;
-    const float kTarget = RESCALE_TARGET;
 
-    v16i S0[2], S1[2];
-
-    // Step j: prefetch K(j+2) and V(j+1), issue the QK^T MFMAs of block j+1
-    // (they run while this wave does the softmax of block j), then P.V of
-    // block j. PAR = j % 2 picks the buffers and the S registers.
-    // k_fill held K(j) and gets K(j+2); k_next holds K(j+1); v_cur holds V(j);
-    // v_fill held V(j-1) and gets V(j+1). sc: S(j), sn: S(j+1).
-    auto step = [&](int blk, uint8_t* k_fill, const uint8_t* k_next, const uint8_t* v_cur, uint8_t* v_fill,
-                    v16i (&sc)[2], v16i (&sn)[2]) __attribute__((always_inline)) {
+    // Softmax of block blk (scores sc, biased by 1.5 * 2^23) and its P.V from
+    // the V tile v_cur: updates m, l and O.
+    auto softmax_pv = [&](int blk, v16i (&sc)[2], const uint8_t* v_cur) __attribute__((always_inline)) {
         // The reference's fp32 operation order for the logits: no FMA contraction.
 #pragma clang fp contract(off)
-        // Workgroup-uniform: does any key of this block need masking?
-        const bool MASK = blk >= nfull;
-        if (blk + 2 < nblk) fetch(kg, blk + 2, k_fill, KCPR);
-        if (blk + 1 < nblk) {
-            fetch(vg, blk + 1, v_fill, 4);
-            qk(k_next, sn);
-        }
-        // Phase fences: keep the scheduler from hoisting the next phase's loads
-        // into this one (which would push the register count past 256).
-        __builtin_amdgcn_sched_barrier(0);
         // q_scale * k_scale, kept above zero so that -inf * scl stays -inf.
         const float scl = fmaxf(qs * ksc[blk], 1.0e-30f);
         const float xoff = -MAGIC * scl;
-        if (MASK) {
+        if (blk >= nfull) {  // workgroup-uniform
             // Keys past the sequence, and keys after the query when causal. Element
             // (t, r) is key blk*BN + 4*half + c with the constant c below, so one
             // per-lane limit decides every element.
@@ -231,35 +208,41 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
                 for (int r = 0; r < 16; r++)
                     if (32 * t + 8 * (r >> 2) + (r & 3) >= lim) sc[t][r] = NEG_INF_BITS;
         }
-        // Row max over this lane's 32 keys, three at a time (v_max3), then the partner half.
-        int mx = max(sc[0][0], sc[1][15]);
+        // Row max over this lane's 32 keys (a v_max3 tree), then the partner half.
+        int m3[11];
 #pragma unroll
-        for (int i = 1; i < 31; i += 2) mx = max(max(mx, sc[i >> 4][i & 15]), sc[(i + 1) >> 4][(i + 1) & 15]);
+        for (int i = 0; i < 10; i++)
+            m3[i] = max(max(sc[(3 * i) >> 4][(3 * i) & 15], sc[(3 * i + 1) >> 4][(3 * i + 1) & 15]),
+                        sc[(3 * i + 2) >> 4][(3 * i + 2) & 15]);
+        m3[10] = max(sc[1][14], sc[1][15]);
+        int mx = max(max(max(max(m3[0], m3[1]), m3[2]), max(max(m3[3], m3[4]), m3[5])),
+                     max(max(max(m3[6], m3[7]), m3[8]), max(m3[9], m3[10])));
         mx = max(mx, swap_halves(mx, sel));
 
-        // The block max in log2 units; the reference point moves only when the
-        // block exceeds it by more than RESCALE_SLACK (then O and l are rescaled).
-        // (a fully masked block gives -inf, which leaves m alone)
-        const float mblk = fmaf(__int_as_float(mx), scl, xoff);
-        const bool grow = mblk > m + RESCALE_SLACK;
-        const float mnew = grow ? mblk : m;
+        // The running max in log2 units (a fully masked block gives -inf,
+        // which leaves m alone); the row's largest score maps to P = 448.
+        const float mnew = fmaxf(m, fmaf(__int_as_float(mx), scl, xoff));
+        const bool grow = mnew > m;
         const float alpha = __builtin_amdgcn_exp2f(m - mnew);
         m = mnew;
 
         // P = 2^(x sc + off) of the biased scores; a masked one is -inf, so
         // (scl > 0) its exp2 is 0.
-        const float off = (kTarget - mnew) + xoff;
+        const float off = (LOG2_448 - mnew) + xoff;
         float p[2][16];
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int r = 0; r < 16; r++) p[t][r] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sc[t][r]), scl, off));
-        float sum = 0.f;
+        // Row sum as a pairwise tree.
+        float q16[16];
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+        for (int r = 0; r < 16; r++) q16[r] = p[0][r] + p[1][r];
 #pragma unroll
-            for (int r = 0; r < 16; r++) sum += p[t][r];
-        l = fmaf(l, alpha, sum);
+        for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+            for (int r = 0; r < w; r++) q16[r] += q16[r + w];
+        l = fmaf(l, alpha, q16[0]);
 
         // P^T operand: register j holds keys of accumulators 4(j%4)..+3 of sub-tile j/4.
         v8i pb;
@@ -270,40 +253,86 @@ __global__ __launch_bounds__(256, 2) void sage_attn(const int8_t* __restrict__ q
             pb[j] = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0 + 2], p[t][r0 + 3], lo, true);
         }
         __builtin_amdgcn_sched_barrier(0);
-        // V^T operands of block j (row = channel, 4 chunks per 64-byte row).
-        uint4 va[DT][2];
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            va[dt][0] = *reinterpret_cast<const uint4*>(v_cur + 16 * 128 * dt + voff0);
-            va[dt][1] = *reinterpret_cast<const uint4*>(v_cur + 16 * 128 * dt + voff1);
-        }
+        // O *= alpha, only when some row of the wave moved its max.
         if (__any(grow)) {
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) o[dt][r] *= alpha;
         }
+        // O^T += V^T P^T, V^T operands (row = channel, 4 chunks per 64-byte
+        // row) read two channel tiles at a time.
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) {
-            const v8i av = {(int)va[dt][0].x, (int)va[dt][0].y, (int)va[dt][0].z, (int)va[dt][0].w,
-                            (int)va[dt][1].x, (int)va[dt][1].y, (int)va[dt][1].z, (int)va[dt][1].w};
-            o[dt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, pb, o[dt], 0, 0, 0, 127, 0, 127);
+        for (int d2 = 0; d2 < DT; d2 += 2) {
+            uint4 va[2][2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                va[e][0] = *reinterpret_cast<const uint4*>(v_cur + 16 * 128 * (d2 + e) + voff0);
+                va[e][1] = *reinterpret_cast<const uint4*>(v_cur + 16 * 128 * (d2 + e) + voff1);
+            }
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const v8i av = {(int)va[e][0].x, (int)va[e][0].y, (int)va[e][0].z, (int)va[e][0].w,
+                                (int)va[e][1].x, (int)va[e][1].y, (int)va[e][1].z, (int)va[e][1].w};
+                o[d2 + e] =
+                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, pb, o[d2 + e], 0, 0, 0, 127, 0, 127);
+            }
         }
-        // Drains this wave's prefetches and publishes them; the buffers read
-        // in this step are free afterwards.
-        __syncthreads();
     };
 
-    fetch(kg, 0, ldsK0, KCPR);
-    fetch(vg, 0, ldsV0, 4);
-    if (nblk > 1) fetch(kg, 1, ldsK1, KCPR);
-    __syncthreads();
-    qk(ldsK0, S0);
-    __syncthreads();  // every wave has read K(0) before step 0 refills its buffer
-
-    for (int blk = 0; blk < nblk; blk += 2) {
-        step(blk, ldsK0, ldsK1, ldsV0, ldsV1, S0, S1);
-        if (blk + 1 < nblk) step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0, S1, S0);
+    v16i S0[2], S1[2];
+    if constexpr (PIPE) {
+        // Step j: prefetch K(j+2) and V(j+1), issue the QK^T MFMAs of block
+        // j+1 (they run while this wave does the softmax of block j), then P.V
+        // of block j. k_fill held K(j) and gets K(j+2); k_next holds K(j+1);
+        // v_cur holds V(j); v_fill held V(j-1) and gets V(j+1). sc: S(j),
+        // sn: S(j+1).
+        auto step = [&](int blk, uint8_t* k_fill, const uint8_t* k_next, const uint8_t* v_cur, uint8_t* v_fill,
+                        v16i (&sc)[2], v16i (&sn)[2]) __attribute__((always_inline)) {
+            if (blk + 2 < nblk) fetch(kg, blk + 2, k_fill, KCPR);
+            if (blk + 1 < nblk) {
+                fetch(vg, blk + 1, v_fill, 4);
+                qk(k_next, sn);
+            }
+            // Phase fence: keeps the scheduler from hoisting the next phase's
+            // loads into this one (which would push the register count past 256).
+            __builtin_amdgcn_sched_barrier(0);
+            softmax_pv(blk, sc, v_cur);
+            // Drains this wave's prefetches and publishes them; the buffers
+            // read in this step are free afterwards.
+            __syncthreads();
+        };
+        fetch(kg, 0, ldsK0, KCPR);
+        fetch(vg, 0, ldsV0, 4);
+        if (nblk > 1) fetch(kg, 1, ldsK1, KCPR);
+        __syncthreads();
+        qk(ldsK0, S0);
+        __syncthreads();  // every wave has read K(0) before step 0 refills its buffer
+        for (int blk = 0; blk < nblk; blk += 2) {
+            step(blk, ldsK0, ldsK1, ldsV0, ldsV1, S0, S1);
+            if (blk + 1 < nblk) step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0, S1, S0);
+        }
+    } else {
+        // Step j: prefetch K(j+1) and V(j+1) into the other buffers, then
+        // QK^T, softmax and P.V of block j; the other waves on the SIMD (three
+        // at this size) fill the MFMA and VALU gaps.
+        auto step = [&](int blk, const uint8_t* k_cur, uint8_t* k_fill, const uint8_t* v_cur, uint8_t* v_fill)
+                        __attribute__((always_inline)) {
+            if (blk + 1 < nblk) {
+                fetch(kg, blk + 1, k_fill, KCPR);
+                fetch(vg, blk + 1, v_fill, 4);
+            }
+            qk(k_cur, S0);
+            softmax_pv(blk, S0, v_cur);
+            __syncthreads();
+        };
+        fetch(kg, 0, ldsK0, KCPR);
+        fetch(vg, 0, ldsV0, 4);
+        __syncthreads();
+        for (int blk = 0; blk < nblk; blk += 2) {
+            step(blk, ldsK0, ldsK1, ldsV0, ldsV1);
+            if (blk + 1 < nblk) step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0);
+        }
     }
 
     // out = O / l * v_scale + v_mean; lane holds channels 32dt + 8j + 4*half + 0..3.
