@@ -10,6 +10,7 @@ is exactly the written operation order.
 """
 from __future__ import annotations
 
+import ctypes
 import os
 import subprocess
 import sys
@@ -63,6 +64,13 @@ def build(verbose: bool = True) -> Path:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
+    # Every kernel the launchers name must be in the library: load it with all
+    # symbols resolved now (a kernel the host pass failed to instantiate shows
+    # up here, not at first use on a GPU box).
+    try:
+        ctypes.CDLL(str(tmp), mode=os.RTLD_NOW)
+    except OSError as e:
+        raise RuntimeError(f"built library does not load: {e}") from e
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")

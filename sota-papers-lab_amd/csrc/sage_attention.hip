@@ -56,6 +56,23 @@ __device__ __forceinline__ int swap_halves(int x, bool first) {
 __device__ __forceinline__ float swap_halves(float x, bool first) {
     return __int_as_float(swap_halves(__float_as_int(x), first));
 }
+// Values the compiler may not re-derive or rematerialise: a uniform pointer
+// stays in SGPRs and is not reassociated with per-lane offsets; a VGPR value
+// stays where it is. (The constraints name AMDGPU register classes, so the
+// statements exist only in the device pass.)
+__device__ __forceinline__ const uint8_t* opaque_uniform(const uint8_t* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+s"(p));
+#endif
+    return p;
+}
+template <typename T>
+__device__ __forceinline__ void opaque_vgpr(T& x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm volatile("" : "+v"(x));
+#endif
+}
+
 // The dispatcher deals workgroups to the 8 XCDs round-robin by linear id,
 // and each XCD has its own L2. Tile t (query tile fastest, then head, then
 // batch) goes to the workgroup that gives XCD x the contiguous range of
@@ -138,11 +155,24 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
     // Direct global -> LDS copy of one tile. Lane `lane` of wave `wave` fills
     // physical chunk c of the tile, so it fetches the logical chunk that the
     // swizzle puts there (swz is an involution).
-    auto fetch = [&](const uint8_t* src_base, int blk, uint8_t* dst, int cpr) __attribute__((always_inline)) {
+    // The tile base is uniform and is kept opaque, so that it stays in SGPRs
+    // and each load takes it plus a 32-bit lane offset (instead of a 64-bit
+    // per-lane address rebuilt every block); the LDS destination is uniform
+    // as well (M0).
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t foff[CPT][2];  // [chunk][K, V]
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+        foff[i][0] = 16u * (uint32_t)swz(i * 256 + wv * 64 + lane, KCPR);
+        foff[i][1] = 16u * (uint32_t)swz(i * 256 + wv * 64 + lane, 4);
+    }
+    auto fetch = [&](const uint8_t* src_base, int blk, uint8_t* dst, int which) __attribute__((always_inline)) {
+        const uint8_t* tb = opaque_uniform(src_base + (long long)blk * TILE);
 #pragma unroll
         for (int i = 0; i < CPT; i++) {
-            const int c0 = i * 256 + wave * 64;
-            __builtin_amdgcn_global_load_lds(src_base + (long long)blk * TILE + 16 * swz(c0 + lane, cpr),
+            const int c0 = i * 256 + wv * 64;
+            opaque_vgpr(foff[i][which]);  // widened next to the load: base + zext(offset) form
+            __builtin_amdgcn_global_load_lds(tb + (size_t)foff[i][which],
                                              (__attribute__((address_space(3))) void*)(dst + 16 * c0), 16, 0, 0);
         }
     };
@@ -163,6 +193,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
     v16i magic;
 #pragma unroll
     for (int r = 0; r < 16; r++) magic[r] = MAGIC_BITS;
+    opaque_vgpr(magic);  // kept in VGPRs, not rebuilt before every block
     auto qk = [&](const uint8_t* kt, v16i (&s)[2]) __attribute__((always_inline)) {
         uint4 ka[2][KS];
 #pragma unroll
@@ -188,6 +219,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
     // m: the row's running max (log2 units); P = 2^(x - m + log2 448).
     float m = -1.0e30f, l = 0.f;
 
+    v8i pb = {};  // P^T operand of the current block
     // Softmax of block blk (scores sc, biased by 1.5 * 2^23) and its P.V from
     // the V tile v_cur: updates m, l and O.
     auto softmax_pv = [&](int blk, v16i (&sc)[2], const uint8_t* v_cur) __attribute__((always_inline)) {
@@ -244,12 +276,13 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
             for (int r = 0; r < w; r++) q16[r] += q16[r + w];
         l = fmaf(l, alpha, q16[0]);
 
-        // P^T operand: register j holds keys of accumulators 4(j%4)..+3 of sub-tile j/4.
-        v8i pb;
+        // P^T operand: register j holds keys of accumulators 4(j%4)..+3 of
+        // sub-tile j/4 (both halves are rewritten, so the previous block's
+        // value serves as the unused input half and needs no zeroing).
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int t = j >> 2, r0 = 4 * (j & 3);
-            const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0], p[t][r0 + 1], 0, false);
+            const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0], p[t][r0 + 1], pb[j], false);
             pb[j] = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0 + 2], p[t][r0 + 3], lo, true);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -289,9 +322,9 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
         // sn: S(j+1).
         auto step = [&](int blk, uint8_t* k_fill, const uint8_t* k_next, const uint8_t* v_cur, uint8_t* v_fill,
                         v16i (&sc)[2], v16i (&sn)[2]) __attribute__((always_inline)) {
-            if (blk + 2 < nblk) fetch(kg, blk + 2, k_fill, KCPR);
+            if (blk + 2 < nblk) fetch(kg, blk + 2, k_fill, 0);
             if (blk + 1 < nblk) {
-                fetch(vg, blk + 1, v_fill, 4);
+                fetch(vg, blk + 1, v_fill, 1);
                 qk(k_next, sn);
             }
             // Phase fence: keeps the scheduler from hoisting the next phase's
@@ -302,9 +335,9 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
             // read in this step are free afterwards.
             __syncthreads();
         };
-        fetch(kg, 0, ldsK0, KCPR);
-        fetch(vg, 0, ldsV0, 4);
-        if (nblk > 1) fetch(kg, 1, ldsK1, KCPR);
+        fetch(kg, 0, ldsK0, 0);
+        fetch(vg, 0, ldsV0, 1);
+        if (nblk > 1) fetch(kg, 1, ldsK1, 0);
         __syncthreads();
         qk(ldsK0, S0);
         __syncthreads();  // every wave has read K(0) before step 0 refills its buffer
@@ -319,15 +352,15 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
         auto step = [&](int blk, const uint8_t* k_cur, uint8_t* k_fill, const uint8_t* v_cur, uint8_t* v_fill)
                         __attribute__((always_inline)) {
             if (blk + 1 < nblk) {
-                fetch(kg, blk + 1, k_fill, KCPR);
-                fetch(vg, blk + 1, v_fill, 4);
+                fetch(kg, blk + 1, k_fill, 0);
+                fetch(vg, blk + 1, v_fill, 1);
             }
             qk(k_cur, S0);
             softmax_pv(blk, S0, v_cur);
             __syncthreads();
         };
-        fetch(kg, 0, ldsK0, KCPR);
-        fetch(vg, 0, ldsV0, 4);
+        fetch(kg, 0, ldsK0, 0);
+        fetch(vg, 0, ldsV0, 1);
         __syncthreads();
         for (int blk = 0; blk < nblk; blk += 2) {
             step(blk, ldsK0, ldsK1, ldsV0, ldsV1);
