@@ -76,6 +76,18 @@ def time_events(torch, stream, fn, reps: int) -> float:
     return a.elapsed_time(b) / reps
 
 
+def measured_traffic(cfg: int):
+    """HBM bytes per attention launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary for this config (copy-calibrated), or None."""
+    import re
+
+    f = ROOT / "profiles" / f"sage_attn_c{cfg}_hbm_traffic.md"
+    if not f.exists():
+        return None
+    m = re.search(rf"traffic_bytes_per_launch sage_attn C{cfg} = ([0-9.eE+]+)", f.read_text())
+    return (float(m.group(1)), str(f.relative_to(ROOT))) if m else None
+
+
 def cpu_baseline(q, k, v, cfg: int, budget_s: float = 12.0) -> dict:
     """The oracle's restatement of the reference arithmetic (prologue + sage
     emulator, oracle/sage_oracle.c) on the host cores, over a bounded sample of
@@ -117,13 +129,15 @@ def cpu_baseline(q, k, v, cfg: int, budget_s: float = 12.0) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    # ~100 warm-up steps: the GPU clock ramps over the first ~60 attention launches
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-peak", action="store_true", help="skip the MFMA peak probes")
-    ap.add_argument("--only", choices=["attend", "prepare"],
-                    help="profiling mode: run only this kernel group --steps times and print its timing")
+    ap.add_argument("--only", choices=["attend", "prepare", "copy"],
+                    help="profiling mode: run only this kernel group --steps times and print its timing "
+                         "(copy: a plain 512 MiB device copy, the reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box here has one GPU); "
@@ -134,6 +148,17 @@ def main() -> int:
     import spl_sage as S
 
     torch.cuda.set_device(0)
+    if args.only == "copy":
+        n = 512 << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        stream = torch.cuda.current_stream()
+        for _ in range(args.warmup):
+            dst.copy_(src)
+        ms = time_events(torch, stream, lambda: dst.copy_(src), args.steps)
+        print(json.dumps({"only": "copy", "bytes_read": n, "bytes_written": n, "ms": round(ms, 4),
+                          "gbs": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return 0
     B, H, HK, N, D, dt, causal, *_ = CONFIGS[args.config]
     q, k, v = synthetic(torch, args.config)
     out = torch.empty((B, N, H, D), dtype=q.dtype, device="cuda")
@@ -186,6 +211,7 @@ def main() -> int:
     n_q, n_kv = B * H * N * D, B * HK * N * D
     pro_bytes = 2 * (n_q + 2 * n_kv) + (n_q + 2 * n_kv) + 4 * (B * H * plan.tq_pad // 16 + B * HK * plan.tk_pad // 64
                                                                + B * HK * 4 * D)
+    traffic = measured_traffic(args.config)
     line = {
         "metric": "attention TOPS @ B2 H32 N4096 D128; % of INT8/FP8 MFMA peak",
         "value": round(value, 2),
@@ -207,8 +233,11 @@ def main() -> int:
         "prologue": {"ms": round(prep_ms, 4), "gbs": round(pro_bytes / (prep_ms * 1e-3) / 1e9, 1),
                      "frac_of_hbm": round(pro_bytes / (prep_ms * 1e-3) / 1e9 / VENDOR_HBM_GBS, 4)},
         "roofline": {"bound": "mfma", "achieved": round(attn_tops, 2), "peak": VENDOR_PEAK_TOPS,
-                     "unit": "TFLOP/s", "frac": round(attn_tops / VENDOR_PEAK_TOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(attn_tops / VENDOR_PEAK_TOPS, 4),
+                     "traffic": traffic[0] if traffic else None},
         "peaks_measured_tops": peaks,
+        "traffic_source": traffic[1] if traffic else None,
+        "attention_hbm_gbs": round(traffic[0] / (attn_ms * 1e-3) / 1e9, 1) if traffic else None,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(q, k, v, args.config)

@@ -1,0 +1,183 @@
+"""Host side of the C ABI on the CPU (no GPU compute): the library loads and
+exports every function include/sage_hip.h declares, the ctypes mirror has
+the C struct layouts, and the plan / stride / tile / flops logic passes the
+reference's own known-answer tests (tests.rs:135-283) and error texts."""
+from __future__ import annotations
+
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "sage_hip.h"
+
+
+@pytest.fixture(scope="module")
+def S():
+    import spl_sage
+
+    return spl_sage
+
+
+def _header_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"^\s*[A-Za-z_][\w \*]*?\b(sage_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_function(S):
+    from spl_sage import _abi
+
+    names = _header_functions()
+    assert len(names) >= 20, names
+    lib = C.CDLL(str(_abi.LIB_PATH))
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python mirror binds each of them with a signature
+    assert sorted(_abi.SIGNATURES) == names
+
+
+def test_ctypes_structs_match_the_c_layout(S, tmp_path):
+    """sizeof / offsetof of every ABI struct, compiled from the header with gcc,
+    equal the ctypes mirror's (the role of geom_matches_the_cuda_struct,
+    tests.rs:234-243, at this boundary)."""
+    from spl_sage import _abi
+
+    structs = {
+        "sage_tile": ["warps", "m_tiles", "stages"],
+        "sage_config": ["tile", "pv_accum"],
+        "sage_shape": ["batch", "heads", "tokens", "kv_heads"],
+        "sage_frame_layout": ["frames", "special", "grid_h", "grid_w", "dense_frames"],
+        "sage_kv_merge": ["stride", "layout"],
+        "sage_plan": ["shape", "merge", "tq_pad", "tk", "tk_pad"],
+        "sage_strides": ["batch", "token", "head"],
+        "sage_tensor": ["data", "len", "strides", "dtype"],
+        "sage_tensor_mut": ["data", "len", "strides", "dtype"],
+        "sage_options": ["softmax_scale", "has_softmax_scale", "smooth_k", "smooth_v", "qk_norm_params",
+                         "qk_norm_len", "qk_norm_eps", "causal"],
+        "sage_ws_buffers": ["q8", "q_scale", "k8", "k_scale", "v8", "stats", "kbias", "q8_len", "q_scale_len",
+                            "k8_len", "k_scale_len", "v8_len", "stats_len", "kbias_len"],
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for s, fields in structs.items():
+        lines.append(f'printf("{s} %zu\\n", sizeof({s}));')
+        for f in fields:
+            lines.append(f'printf("{s}.{f} %zu\\n", offsetof({s}, {f}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-o", str(exe), str(src)], check=True)
+    got = dict(l.split() for l in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                 text=True).stdout.splitlines())
+    for s, fields in structs.items():
+        cls = getattr(_abi, s)
+        assert int(got[s]) == C.sizeof(cls), s
+        for f in fields:
+            assert int(got[f"{s}.{f}"]) == getattr(cls, f).offset, f"{s}.{f}"
+
+
+def test_vggt_dense_geometry(S):
+    """tests.rs:137-148: 200 frames x 689 tokens."""
+    plan = S.Plan.new(S.Shape(1, 16, 200 * 689))
+    assert (plan.tq_pad, plan.tk, plan.tk_pad) == (137856, 137800, 137856)
+
+
+def _vggt_layout(S, frames: int, dense_frames: int = 0):
+    return S.FrameLayout(frames, 17, 21, 32, dense_frames)
+
+
+def test_vggt_merge_key_counts(S):
+    """tests.rs:149-152 and :96-110: merged key counts of the pooled layouts."""
+    layout = _vggt_layout(S, 200)
+    assert layout.tokens_per_frame() == 689
+    shape = S.Shape(1, 16, 200 * 689)
+    assert S.Plan.new(shape, S.KvMerge.Pool(2, layout)).tk == 200 * (17 + 11 * 16)
+    assert S.Plan.new(shape, S.KvMerge.Pool(4, layout)).tk == 200 * (17 + 6 * 8)
+    dense1 = _vggt_layout(S, 3, dense_frames=1)
+    assert S.Plan.new(S.Shape(1, 1, 3 * 689), S.KvMerge.Pool(4, dense1)).tk == 689 + 2 * 65
+
+
+def test_plan_rejects_bad_layouts(S):
+    """tests.rs:175-190, with the reference's error texts."""
+    layout = _vggt_layout(S, 2)
+    with pytest.raises(S.SageError, match="frame layout"):
+        S.Plan.new(S.Shape(1, 2, 1000), S.KvMerge.Pool(2, layout))
+    shape = S.Shape(1, 2, 2 * 689)
+    with pytest.raises(S.SageError, match="KV merge stride must be 2 or 4, got 3"):
+        S.Plan.new(shape, S.KvMerge.Pool(3, layout))
+    S.Plan.new(shape, S.KvMerge.Pool(4, layout))
+    with pytest.raises(S.SageError, match="empty attention shape"):
+        S.Plan.new(S.Shape(1, 2, 0))
+
+
+def test_plan_padding_and_tails(S):
+    """mod.rs:431-434: tq_pad to 128, tk_pad to 64; the C5 tail shape."""
+    p = S.Plan.new(S.Shape(1, 48, 17776))
+    assert (p.tq_pad, p.tk, p.tk_pad) == (17792, 17776, 17792)
+    assert p.q_tiles() == 139 and p.kblocks() == 278
+    p = S.Plan.new(S.Shape(2, 32, 4096))
+    assert (p.tq_pad, p.tk_pad) == (4096, 4096)
+
+
+def test_plan_rejects_bad_grouped_heads(S):
+    with pytest.raises(S.SageError):
+        S.Plan.new(S.Shape(1, 32, 128, kv_heads=5))
+    assert S.Plan.new(S.Shape(1, 32, 128, kv_heads=8)).kv_heads() == 8
+
+
+def test_strides_cover_the_tensor(S):
+    """tests.rs:245-261."""
+    shape = S.Shape(2, 3, 5)
+    d = 64
+    assert S.Strides.bthd(5, 3, d).extent(shape, d) == 2 * 5 * 3 * d
+    assert S.Strides.bhtd(5, 3, d).extent(shape, d) == 2 * 3 * 5 * d
+    assert S.Strides.packed_qkv(5, 3, d).extent(shape, d) + 2 * 3 * d == 2 * 5 * 3 * 3 * d
+    with pytest.raises(S.SageError, match="x strides must be multiples of 8 elements"):
+        S.Strides.bthd(5, 3, 60).check("x")
+
+
+def test_flops_counts_the_metric(S):
+    """mod.rs:905-910 (4 B H Tq Tk D); causal counts the visible half, 2 B H D N (N + 1)."""
+    c2 = S.Plan.new(S.Shape(2, 32, 4096))
+    assert S.flops(c2, 128) == 4.0 * 2 * 32 * 4096 * 4096 * 128
+    assert abs(S.flops(c2, 128) - 5.498e11) / 5.498e11 < 1e-3
+    c3 = S.Plan.new(S.Shape(1, 32, 16384))
+    assert S.flops(c3, 128, causal=True) == 2.0 * 32 * 128 * 16384 * 16385
+    c1 = S.Plan.new(S.Shape(1, 2, 256))
+    assert S.flops(c1, 64) == 4.0 * 2 * 256 * 256 * 64  # 3.36e7
+
+
+def test_v8_position_is_the_operand_permutation(S):
+    """Every key of a 64-key block has one byte in its V^T row, and key k sits
+    where lane-half g = (k >> 2) & 1, register (k >> 5) * 4 + ((k >> 3) & 3),
+    byte k & 3 of the FP8 B operand puts it."""
+    pos = [S.v8_position(k) for k in range(64)]
+    assert sorted(pos) == list(range(64))
+    for k in range(64):
+        g, reg, byte = (k >> 2) & 1, (k >> 5) * 4 + ((k >> 3) & 3), k & 3
+        assert pos[k] == 32 * g + 4 * reg + byte
+
+
+def test_tile_menu_and_errors(S):
+    """mod.rs:116-168: the per-head-dim default tile validates; others are refused
+    with the reference's message."""
+    for d in (64, 128):
+        cfg = S.Config.for_head_dim(d)
+        cfg.tile.validate()
+        assert cfg.tile.rows() == 128
+    with pytest.raises(S.SageError, match="unsupported sage tile"):
+        S.Tile(3, 1, 2).validate()
+
+
+def test_device_gate_without_a_gpu(S):
+    """check_device reports, without a GPU, a device error rather than crashing."""
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(S.SageError):
+        S.check_device(0)
