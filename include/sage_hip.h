@@ -10,7 +10,7 @@
  *   - every call enqueues on the context's stream and returns without
  *     synchronising (mod.rs:509-510); prepare/attend neither allocate nor
  *     synchronise, so they can be captured in a hipGraph (the workspace is
- *     allocated once per shape by sage_workspace, mod.rs:649-670);
+ *     allocated once per shape by sage_workspace_new, mod.rs:649-670);
  *   - every invalid input is reported before any launch, with the reference's
  *     error text, through the return status and sage_last_error()
  *     (mod.rs:251-259,405-440,587-589,681-709,841-852);

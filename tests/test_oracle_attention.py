@@ -117,3 +117,18 @@ def test_fast_logit_shift_is_small_at_baseline_scale(oracle):
     ulp = np.spacing(np.float32(12582912.0 * sc_max))
     # a common factor 2^(shift) per block moves out by at most |out| * (2^(2 ulp) - 1) + E4M3 tie flips
     assert e["max_abs"] <= float(np.abs(b).max()) * (2.0 ** (2 * ulp) - 1) + 0.05, (e, ulp)
+
+
+def test_f64_attention_closed_forms(oracle):
+    """Textbook attention: constant V rows give that constant for every query
+    (the weights sum to 1), and a causal row 0 sees only key 0."""
+    p, g = oracle.config(1, seed=5)
+    q, k, v = oracle.generate(p, g)
+    c = oracle.encode16(np.array([1.75], np.float32), p.dtype)[0]
+    vc = np.full_like(v, c)
+    out = oracle.attention_f64(p, q, k, vc)
+    np.testing.assert_allclose(out, 1.75, rtol=1e-6)
+    p.causal = True
+    out = oracle.attention_f64(p, q, k, v, rows=np.array([0], np.int32))
+    v0 = oracle.decode16(v[:, 0], p.dtype)  # [B, HK, D]
+    np.testing.assert_allclose(out[:, :, 0], v0, rtol=1e-6, atol=1e-7)
