@@ -1,4 +1,4 @@
-"""Benchmark of the gfx950 SageAttention2 forward path (BASELINE.json metric:
+"""Benchmark of the gfx950 SageAttention2 forward path (headline metric:
 "attention TOPS @ B2 H32 N4096 D128; % of INT8/FP8 MFMA peak").
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--no-cpu]
@@ -26,7 +26,7 @@ sys.path.insert(0, str(ROOT / "sota-papers-lab_amd"))
 VENDOR_PEAK_TOPS = 5000.0   # MI355X dense INT8 (POPS) and FP8 (PFLOPS) MFMA, x1000
 VENDOR_HBM_GBS = 8000.0
 
-# BASELINE.json configs as (B, H, HKV, N, D, dtype, causal, k_off_std, outlier_ch, outlier_scale, tok_frac, tok_scale)
+# Benchmark configurations C1-C5 as (B, H, HKV, N, D, dtype, causal, k_off_std, outlier_ch, outlier_scale, tok_frac, tok_scale)
 CONFIGS = {
     1: (1, 2, 2, 256, 64, "f16", False, 2.0, 0, 1.0, 0.0, 1.0),
     2: (2, 32, 32, 4096, 128, "bf16", False, 2.0, 0, 1.0, 0.0, 1.0),
@@ -45,7 +45,7 @@ NAMES = {
 
 def synthetic(torch, cfg: int, seed: int = 0):
     """Q, V ~ N(0,1); K ~ N(0,1) * s + off[h][c] (off ~ N(0, k_off_std)), as the
-    BASELINE configs describe; generated on the GPU, layout [B][N][H][D]."""
+    configurations describe; generated on the GPU, layout [B][N][H][D]."""
     B, H, HK, N, D, dt, _, koff, och, osc, tfrac, tsc = CONFIGS[cfg]
     g = torch.Generator(device="cuda").manual_seed(seed)
     tdt = torch.bfloat16 if dt == "bf16" else torch.float16

@@ -17,9 +17,9 @@
  *   - the caller owns Q/K/V/out device memory (borrowed for the call); the
  *     library owns the workspace and frees it in sage_workspace_destroy.
  *
- * Extensions with no reference counterpart: fp16 inputs
- * and output (dtype fields), causal masking (sage_options.causal) and
- * grouped-query heads (sage_shape.kv_heads).
+ * Extensions with no reference counterpart (needed by the benchmark
+ * configurations): fp16 inputs and output (dtype fields), causal masking
+ * (sage_options.causal) and grouped-query heads (sage_shape.kv_heads).
  */
 #ifndef SAGE_HIP_H
 #define SAGE_HIP_H

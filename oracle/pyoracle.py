@@ -285,7 +285,7 @@ def errors(ours: np.ndarray, ref: np.ndarray) -> dict:
     return dict(cos=o[0], rel_l1=o[1], rel_l2=o[2], max_abs=o[3], ref_max=o[4])
 
 
-# The BASELINE configs (BASELINE.json "configs"), as (Problem, GenSpec).
+# The five benchmark configurations C1-C5, as (Problem, GenSpec).
 def config(n: int, seed: int = 1):
     if n == 1:
         return Problem(1, 2, 256, 64, dtype=F16), GenSpec(k_off_std=2.0, seed=seed)

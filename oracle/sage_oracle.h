@@ -14,8 +14,8 @@
  *   - sage emulator     cuda/sage_attn.cu:262-344,402-421 semantics
  *   - error metrics     src/sage/reference.rs:202-225
  *
- * Pinning status of each function is listed in oracle/README.md (the header
- * of each function in sage_oracle.c says what pins it).
+ * The header of each function in sage_oracle.c says what pins it; the
+ * checks themselves are tests/test_oracle_*.py.
  */
 #ifndef SAGE_ORACLE_H
 #define SAGE_ORACLE_H

@@ -96,7 +96,7 @@ def test_fp16_output_from_bf16_inputs(oracle, torch_gpu):
 
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
 def test_baseline_configs(oracle, torch_gpu, cfg):
-    """BASELINE.json configs at full size: prologue bit-exact over every
+    """The benchmark configurations C1-C5 at full size: prologue bit-exact over every
     element; attention on sampled rows of every (batch, head)."""
     p, g = oracle.config(cfg, seed=100 + cfg)
     q, k, v = oracle.generate(p, g)
