@@ -32,9 +32,16 @@
 // - O accumulates on the MFMA in fp32 across blocks (O = alpha * O + P.V):
 //   the MFMA adds its product to C exactly in fp32, so the reference's
 //   separate per-block fp32 partial is not needed.
-// - K and V tiles are double-buffered in LDS with an XOR swizzle, filled by
-//   direct global -> LDS loads (no staging registers); the next block's copy
-//   is issued before the current block's MFMAs.
+// - K and V tiles are double-buffered in LDS with an XOR swizzle over
+//   256-byte lines (conflict-free b128 operand reads), filled by direct
+//   global -> LDS loads from a uniform SGPR base (no staging registers).
+// - Head dim 128 runs two stages deep: a step issues P.V of the previous
+//   block and QK^T of the next on the MFMA pipe, interleaved by the
+//   scheduler with the current block's softmax on the VALU, so one wave
+//   keeps both pipes busy (two waves a SIMD). Head dim 64 runs one block at
+//   a time with four waves a SIMD instead.
+// - Workgroups are dealt to XCDs so that the ones sharing a head's K and V
+//   share an L2.
 #include "sage_device.hpp"
 #include "sage_internal.hpp"
 
@@ -45,6 +52,8 @@ constexpr int MAGIC_BITS = 0x4B400000;      // bits of 1.5 * 2^23
 constexpr float MAGIC = 12582912.0f;        // 1.5 * 2^23
 constexpr int NEG_INF_BITS = (int)0xFF800000;  // -inf: below every biased score as an int
 constexpr float LOG2_448 = 8.807354922057604f;  // P = 448 for the row max: E4M3's largest finite
+// VALU instructions the scheduler places between consecutive MFMAs of a step.
+constexpr int VALU_PER_MFMA = 12;
 
 // Value of lane ^ 32 (the other half of the wave) with one v_permlane32_swap.
 // The swap returns both operands' new values; in each half of the wave one of
@@ -219,16 +228,18 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
     // m: the row's running max (log2 units); P = 2^(x - m + log2 448).
     float m = -1.0e30f, l = 0.f;
 
-    v8i pb = {};  // P^T operand of the current block
-    // Softmax of block blk (scores sc, biased by 1.5 * 2^23) and its P.V from
-    // the V tile v_cur: updates m, l and O.
-    auto softmax_pv = [&](int blk, v16i (&sc)[2], const uint8_t* v_cur) __attribute__((always_inline)) {
+    v8i pb = {};  // P^T operand of the block whose P.V is next
+
+    // Softmax of block blk (scores sc, biased by 1.5 * 2^23): updates m and l,
+    // writes the P^T operand into pn and returns alpha = 2^(m_old - m_new);
+    // grow says whether this row's max moved.
+    auto softmax = [&](int blk, v16i (&sc)[2], bool masked, v8i& pn, bool& grow) __attribute__((always_inline)) {
         // The reference's fp32 operation order for the logits: no FMA contraction.
 #pragma clang fp contract(off)
         // q_scale * k_scale, kept above zero so that -inf * scl stays -inf.
         const float scl = fmaxf(qs * ksc[blk], 1.0e-30f);
         const float xoff = -MAGIC * scl;
-        if (blk >= nfull) {  // workgroup-uniform
+        if (masked) {
             // Keys past the sequence, and keys after the query when causal. Element
             // (t, r) is key blk*BN + 4*half + c with the constant c below, so one
             // per-lane limit decides every element.
@@ -254,7 +265,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
         // The running max in log2 units (a fully masked block gives -inf,
         // which leaves m alone); the row's largest score maps to P = 448.
         const float mnew = fmaxf(m, fmaf(__int_as_float(mx), scl, xoff));
-        const bool grow = mnew > m;
+        grow = mnew > m;
         const float alpha = __builtin_amdgcn_exp2f(m - mnew);
         m = mnew;
 
@@ -277,73 +288,112 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
         l = fmaf(l, alpha, q16[0]);
 
         // P^T operand: register j holds keys of accumulators 4(j%4)..+3 of
-        // sub-tile j/4 (both halves are rewritten, so the previous block's
+        // sub-tile j/4 (both halves are rewritten, so the register's previous
         // value serves as the unused input half and needs no zeroing).
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int t = j >> 2, r0 = 4 * (j & 3);
-            const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0], p[t][r0 + 1], pb[j], false);
-            pb[j] = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0 + 2], p[t][r0 + 3], lo, true);
+            const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0], p[t][r0 + 1], pn[j], false);
+            pn[j] = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0 + 2], p[t][r0 + 3], lo, true);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        // O *= alpha, only when some row of the wave moved its max.
+        return alpha;
+    };
+    // O *= alpha, only when some row of the wave moved its max.
+    auto rescale = [&](float alpha, bool grow) __attribute__((always_inline)) {
         if (__any(grow)) {
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) o[dt][r] *= alpha;
         }
-        // O^T += V^T P^T, V^T operands (row = channel, 4 chunks per 64-byte
-        // row) read two channel tiles at a time.
+    };
+    // O^T += V^T P^T; V^T operands (row = channel, 4 chunks per 64-byte row)
+    // read two channel tiles at a time.
+    auto pv = [&](const uint8_t* vt, const v8i& pbx) __attribute__((always_inline)) {
 #pragma unroll
         for (int d2 = 0; d2 < DT; d2 += 2) {
             uint4 va[2][2];
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                va[e][0] = *reinterpret_cast<const uint4*>(v_cur + 16 * 128 * (d2 + e) + voff0);
-                va[e][1] = *reinterpret_cast<const uint4*>(v_cur + 16 * 128 * (d2 + e) + voff1);
+                va[e][0] = *reinterpret_cast<const uint4*>(vt + 16 * 128 * (d2 + e) + voff0);
+                va[e][1] = *reinterpret_cast<const uint4*>(vt + 16 * 128 * (d2 + e) + voff1);
             }
 #pragma unroll
             for (int e = 0; e < 2; e++) {
                 const v8i av = {(int)va[e][0].x, (int)va[e][0].y, (int)va[e][0].z, (int)va[e][0].w,
                                 (int)va[e][1].x, (int)va[e][1].y, (int)va[e][1].z, (int)va[e][1].w};
                 o[d2 + e] =
-                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, pb, o[d2 + e], 0, 0, 0, 127, 0, 127);
+                    __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, pbx, o[d2 + e], 0, 0, 0, 127, 0, 127);
             }
         }
+    };
+    // One whole block, unpipelined: softmax, rescale, P.V.
+    auto softmax_pv = [&](int blk, v16i (&sc)[2], const uint8_t* v_cur) __attribute__((always_inline)) {
+        bool grow;
+        const float alpha = softmax(blk, sc, blk >= nfull, pb, grow);
+        __builtin_amdgcn_sched_barrier(0);
+        rescale(alpha, grow);
+        pv(v_cur, pb);
     };
 
     v16i S0[2], S1[2];
     if constexpr (PIPE) {
-        // Step j: prefetch K(j+2) and V(j+1), issue the QK^T MFMAs of block
-        // j+1 (they run while this wave does the softmax of block j), then P.V
-        // of block j. k_fill held K(j) and gets K(j+2); k_next holds K(j+1);
-        // v_cur holds V(j); v_fill held V(j-1) and gets V(j+1). sc: S(j),
-        // sn: S(j+1).
-        auto step = [&](int blk, uint8_t* k_fill, const uint8_t* k_next, const uint8_t* v_cur, uint8_t* v_fill,
+        // Blocks [0, J) with every key visible (J even) run two stages deep:
+        // step j issues P.V of block j-1 and QK^T of block j+1 on the MFMA
+        // pipe, interleaved with block j's softmax on the VALU, so one wave
+        // keeps both busy. K(j+2) and V(j) arrive meanwhile: k_fill held K(j),
+        // k_next holds K(j+1); v_prev holds V(j-1), v_fill held V(j-2).
+        // sc: S(j), sn: S(j+1).
+        auto step = [&](int blk, uint8_t* k_fill, const uint8_t* k_next, uint8_t* v_fill, const uint8_t* v_prev,
                         v16i (&sc)[2], v16i (&sn)[2]) __attribute__((always_inline)) {
-            if (blk + 2 < nblk) fetch(kg, blk + 2, k_fill, 0);
-            if (blk + 1 < nblk) {
-                fetch(vg, blk + 1, v_fill, 1);
-                qk(k_next, sn);
+            fetch(kg, min(blk + 2, nblk - 1), k_fill, 0);
+            fetch(vg, blk, v_fill, 1);
+            pv(v_prev, pb);
+            qk(k_next, sn);
+            v8i pn = pb;
+            bool grow;
+            const float alpha = softmax(blk, sc, false, pn, grow);
+            // MFMAs spread through the softmax: all operand reads first, then
+            // one MFMA per ~VALU_PER_MFMA VALU instructions.
+            __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT + 2 * KS, 0);
+#pragma unroll
+            for (int i = 0; i < DT + 2 * KS; i++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER_MFMA, 0);
             }
-            // Phase fence: keeps the scheduler from hoisting the next phase's
-            // loads into this one (which would push the register count past 256).
+            // Pin the softmax results here, so that the compiler does not sink
+            // their computation past the barrier (out of the interleaved region).
+            opaque_vgpr(pn);
+            opaque_vgpr(l);
             __builtin_amdgcn_sched_barrier(0);
-            softmax_pv(blk, sc, v_cur);
-            // Drains this wave's prefetches and publishes them; the buffers
-            // read in this step are free afterwards.
-            __syncthreads();
+            pb = pn;
+            rescale(alpha, grow);  // after P.V(j-1), before P.V(j)
+            __syncthreads();       // drains this wave's prefetches and publishes them
         };
+        const int J = nfull & ~1;
+        // V1 stands for V(-1): P is zero, and so must its codes be (0 x NaN).
+        {
+            uint4* z = reinterpret_cast<uint4*>(ldsV1);
+            for (int c = tid; c < TILE / 16; c += 256) z[c] = make_uint4(0, 0, 0, 0);
+        }
         fetch(kg, 0, ldsK0, 0);
-        fetch(vg, 0, ldsV0, 1);
-        if (nblk > 1) fetch(kg, 1, ldsK1, 0);
+        fetch(kg, min(1, nblk - 1), ldsK1, 0);
         __syncthreads();
         qk(ldsK0, S0);
         __syncthreads();  // every wave has read K(0) before step 0 refills its buffer
-        for (int blk = 0; blk < nblk; blk += 2) {
+        for (int blk = 0; blk < J; blk += 2) {
             step(blk, ldsK0, ldsK1, ldsV0, ldsV1, S0, S1);
-            if (blk + 1 < nblk) step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0, S1, S0);
+            step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0, S1, S0);
+        }
+        pv(ldsV1, pb);  // P.V(J-1) (with J = 0: zero codes times P = 0)
+        // The rest (masked blocks, and an odd last unmasked one), one at a time.
+        for (int blk = J; blk < nblk; blk++) {
+            __syncthreads();  // every wave is done with K0 and V0
+            fetch(kg, blk, ldsK0, 0);
+            fetch(vg, blk, ldsV0, 1);
+            __syncthreads();
+            qk(ldsK0, S0);
+            softmax_pv(blk, S0, ldsV0);
         }
     } else {
         // Step j: prefetch K(j+1) and V(j+1) into the other buffers, then

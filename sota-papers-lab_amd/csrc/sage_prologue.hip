@@ -156,39 +156,48 @@ __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q,
 }
 
 // sage_quant.cu:163-206 (sg_finalize): even and odd tiles folded separately.
+// One thread per (statistic, channel); the tile partials are loaded sixteen
+// at a time (eight even/odd pairs in flight) and folded in tile order.
 template <int D>
-__global__ __launch_bounds__(256) void sage_finalize(const float* __restrict__ part, float* __restrict__ stats,
-                                                     Geom g) {
+__global__ __launch_bounds__(4 * D) void sage_finalize(const float* __restrict__ part, float* __restrict__ stats,
+                                                       Geom g) {
+    constexpr int BATCH = 8;  // even/odd pairs loaded before folding
     const int hk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
     const long long bhk = (long long)b * g.kv_heads + hk;
     __shared__ float st[4][D];
-    for (int c = tid; c < 4 * D; c += 256) {
-        const int stat = c / D, d = c % D;
+    {
+        const int stat = tid / D, d = tid % D;
         const float* p = part + bhk * g.q_tiles * 4 * D + stat * D + d;
         float r0 = stat < 2 ? 0.f : (stat == 2 ? 3.0e38f : -3.0e38f);
         float r1 = r0;
-        int t = 0;
-        for (; t + 1 < g.q_tiles; t += 2) {
-            const float x0 = p[(long long)t * 4 * D], x1 = p[(long long)(t + 1) * 4 * D];
-            if (stat < 2) {
-                r0 += x0;
-                r1 += x1;
-            } else if (stat == 2) {
-                r0 = fminf(r0, x0);
-                r1 = fminf(r1, x1);
-            } else {
-                r0 = fmaxf(r0, x0);
-                r1 = fmaxf(r1, x1);
+        auto fold = [&](float& r, float x) {
+            r = stat < 2 ? r + x : (stat == 2 ? fminf(r, x) : fmaxf(r, x));
+        };
+        const int pairs = g.q_tiles / 2;
+        int t2 = 0;
+        for (; t2 + BATCH <= pairs; t2 += BATCH) {
+            float x0[BATCH], x1[BATCH];
+#pragma unroll
+            for (int i = 0; i < BATCH; i++) {
+                x0[i] = p[(long long)(2 * (t2 + i)) * 4 * D];
+                x1[i] = p[(long long)(2 * (t2 + i) + 1) * 4 * D];
+            }
+#pragma unroll
+            for (int i = 0; i < BATCH; i++) {
+                fold(r0, x0[i]);
+                fold(r1, x1[i]);
             }
         }
-        if (t < g.q_tiles) {
-            const float x0 = p[(long long)t * 4 * D];
-            r0 = stat < 2 ? r0 + x0 : (stat == 2 ? fminf(r0, x0) : fmaxf(r0, x0));
+        for (; t2 < pairs; t2++) {
+            fold(r0, p[(long long)(2 * t2) * 4 * D]);
+            fold(r1, p[(long long)(2 * t2 + 1) * 4 * D]);
         }
+        if (g.q_tiles & 1) fold(r0, p[(long long)(g.q_tiles - 1) * 4 * D]);
         st[stat][d] = stat < 2 ? r0 + r1 : (stat == 2 ? fminf(r0, r1) : fmaxf(r0, r1));
     }
     __syncthreads();
-    for (int d = tid; d < D; d += 256) {
+    if (tid < D) {
+        const int d = tid;
         const float n = (float)g.tokens;
         const float mk = (g.flags & F_SMOOTH_K) ? st[0][d] / n : 0.f;
         const float mv = (g.flags & F_SMOOTH_V) ? st[1][d] / n : 0.f;
@@ -284,7 +293,7 @@ static hipError_t launch_prologue_d(const uint16_t* q, const uint16_t* k, const 
                        w.q_scale, w.part, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(sage_finalize<D>, dim3(g.kv_heads, g.batch), dim3(256), 0, s, w.part, w.stats, g);
+    hipLaunchKernelGGL(sage_finalize<D>, dim3(g.kv_heads, g.batch), dim3(4 * D), 0, s, w.part, w.stats, g);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(sage_quant_kv<D>, dim3(g.kblocks, g.kv_heads, g.batch), dim3(256), 0, s, k, v, w.stats, w.k8,
