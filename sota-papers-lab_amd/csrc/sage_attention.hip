@@ -35,11 +35,9 @@
 // - K and V tiles are double-buffered in LDS with an XOR swizzle over
 //   256-byte lines (conflict-free b128 operand reads), filled by direct
 //   global -> LDS loads from a uniform SGPR base (no staging registers).
-// - Head dim 128 runs two stages deep: a step issues P.V of the previous
-//   block and QK^T of the next on the MFMA pipe, interleaved by the
-//   scheduler with the current block's softmax on the VALU, so one wave
-//   keeps both pipes busy (two waves a SIMD). Head dim 64 runs one block at
-//   a time with four waves a SIMD instead.
+// - A wave runs one block at a time (QK^T, softmax, P.V); the other waves on
+//   its SIMD fill the MFMA and VALU gaps: three a SIMD at head dim 128 (its
+//   Q^T operands wait in LDS to make room), four at head dim 64.
 // - Workgroups are dealt to XCDs so that the ones sharing a head's K and V
 //   share an L2.
 #include "sage_device.hpp"
@@ -52,8 +50,6 @@ constexpr int MAGIC_BITS = 0x4B400000;      // bits of 1.5 * 2^23
 constexpr float MAGIC = 12582912.0f;        // 1.5 * 2^23
 constexpr int NEG_INF_BITS = (int)0xFF800000;  // -inf: below every biased score as an int
 constexpr float LOG2_448 = 8.807354922057604f;  // P = 448 for the row max: E4M3's largest finite
-// VALU instructions the scheduler places between consecutive MFMAs of a step.
-constexpr int VALU_PER_MFMA = 12;
 
 // Value of lane ^ 32 (the other half of the wave) with one v_permlane32_swap.
 // The swap returns both operands' new values; in each half of the wave one of
@@ -100,15 +96,15 @@ __device__ __forceinline__ bool half_selector(int lane) {
 }
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* __restrict__ q8, const float* __restrict__ q_scale,
+__global__ __launch_bounds__(256, 3) void sage_attn(const int8_t* __restrict__ q8, const float* __restrict__ q_scale,
                                                     const int8_t* __restrict__ k8,
                                                     const float* __restrict__ k_scale,
                                                     const uint8_t* __restrict__ v8, const float* __restrict__ stats,
                                                     uint16_t* __restrict__ out, Geom g) {
     constexpr int BN = ATTN_BN;
-    // Head dim 128 pipelines QK^T one block ahead (two waves a SIMD); head dim
-    // 64 fits three waves a SIMD without it.
-    constexpr bool PIPE = D == 128;
+    // Head dim 128 keeps its Q^T operands in LDS (three waves a SIMD fit in
+    // the registers then); head dim 64 keeps them in registers (four waves).
+    constexpr bool Q_IN_LDS = D == 128;
     constexpr int KS = D / 32;            // INT8 k-steps of 32 channels
     constexpr int DT = D / 32;            // 32-channel tiles of O^T
     constexpr int TILE = BN * D;          // bytes of one K tile and of one V tile
@@ -124,6 +120,8 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
     __shared__ __attribute__((aligned(16))) uint8_t ldsK1[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t ldsV0[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t ldsV1[TILE];
+    // Q^T operands, [wave][k-step][lane] (head dim 128 only).
+    __shared__ v4i ldsQ[Q_IN_LDS ? 4 : 1][KS][64];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 31, half = lane >> 5;
     const int ntq = gridDim.x;
@@ -146,8 +144,13 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
     // Consume the Q loads here, before the first barrier: otherwise the
     // compiler sinks them into the key loop and waits for every outstanding
     // load there, prefetches included.
+    if constexpr (Q_IN_LDS) {
 #pragma unroll
-    for (int s = 0; s < KS; s++) asm volatile("" ::"v"(qa[s]));
+        for (int s = 0; s < KS; s++) ldsQ[wave][s][lane] = qa[s];
+    } else {
+#pragma unroll
+        for (int s = 0; s < KS; s++) asm volatile("" ::"v"(qa[s]));
+    }
     asm volatile("" ::"v"(qs));
 
     int nblk = g.kblocks;
@@ -204,6 +207,9 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
     for (int r = 0; r < 16; r++) magic[r] = MAGIC_BITS;
     opaque_vgpr(magic);  // kept in VGPRs, not rebuilt before every block
     auto qk = [&](const uint8_t* kt, v16i (&s)[2]) __attribute__((always_inline)) {
+        v4i qb[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) qb[ks] = Q_IN_LDS ? ldsQ[wave][ks][lane] : qa[ks];
         uint4 ka[2][KS];
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
 #pragma unroll
             for (int ks = 0; ks < KS; ks++) {
                 const v4i av = {(int)ka[t][ks].x, (int)ka[t][ks].y, (int)ka[t][ks].z, (int)ka[t][ks].w};
-                s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qa[ks], ks ? s[t] : magic, 0, 0, 0);
+                s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qb[ks], ks ? s[t] : magic, 0, 0, 0);
             }
         }
     };
@@ -336,86 +342,26 @@ __global__ __launch_bounds__(256, D == 64 ? 3 : 2) void sage_attn(const int8_t* 
         pv(v_cur, pb);
     };
 
-    v16i S0[2], S1[2];
-    if constexpr (PIPE) {
-        // Blocks [0, J) with every key visible (J even) run two stages deep:
-        // step j issues P.V of block j-1 and QK^T of block j+1 on the MFMA
-        // pipe, interleaved with block j's softmax on the VALU, so one wave
-        // keeps both busy. K(j+2) and V(j) arrive meanwhile: k_fill held K(j),
-        // k_next holds K(j+1); v_prev holds V(j-1), v_fill held V(j-2).
-        // sc: S(j), sn: S(j+1).
-        auto step = [&](int blk, uint8_t* k_fill, const uint8_t* k_next, uint8_t* v_fill, const uint8_t* v_prev,
-                        v16i (&sc)[2], v16i (&sn)[2]) __attribute__((always_inline)) {
-            fetch(kg, min(blk + 2, nblk - 1), k_fill, 0);
-            fetch(vg, blk, v_fill, 1);
-            pv(v_prev, pb);
-            qk(k_next, sn);
-            v8i pn = pb;
-            bool grow;
-            const float alpha = softmax(blk, sc, false, pn, grow);
-            // MFMAs spread through the softmax: all operand reads first, then
-            // one MFMA per ~VALU_PER_MFMA VALU instructions.
-            __builtin_amdgcn_sched_group_barrier(0x100, 2 * DT + 2 * KS, 0);
-#pragma unroll
-            for (int i = 0; i < DT + 2 * KS; i++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, VALU_PER_MFMA, 0);
-            }
-            // Pin the softmax results here, so that the compiler does not sink
-            // their computation past the barrier (out of the interleaved region).
-            opaque_vgpr(pn);
-            opaque_vgpr(l);
-            __builtin_amdgcn_sched_barrier(0);
-            pb = pn;
-            rescale(alpha, grow);  // after P.V(j-1), before P.V(j)
-            __syncthreads();       // drains this wave's prefetches and publishes them
-        };
-        const int J = nfull & ~1;
-        // V1 stands for V(-1): P is zero, and so must its codes be (0 x NaN).
-        {
-            uint4* z = reinterpret_cast<uint4*>(ldsV1);
-            for (int c = tid; c < TILE / 16; c += 256) z[c] = make_uint4(0, 0, 0, 0);
+    v16i S0[2];
+    // Step j: prefetch K(j+1) and V(j+1) into the other buffers, then
+    // QK^T, softmax and P.V of block j; the other waves on the SIMD fill the
+    // MFMA and VALU gaps.
+    auto step = [&](int blk, const uint8_t* k_cur, uint8_t* k_fill, const uint8_t* v_cur, uint8_t* v_fill)
+                    __attribute__((always_inline)) {
+        if (blk + 1 < nblk) {
+            fetch(kg, blk + 1, k_fill, 0);
+            fetch(vg, blk + 1, v_fill, 1);
         }
-        fetch(kg, 0, ldsK0, 0);
-        fetch(kg, min(1, nblk - 1), ldsK1, 0);
+        qk(k_cur, S0);
+        softmax_pv(blk, S0, v_cur);
         __syncthreads();
-        qk(ldsK0, S0);
-        __syncthreads();  // every wave has read K(0) before step 0 refills its buffer
-        for (int blk = 0; blk < J; blk += 2) {
-            step(blk, ldsK0, ldsK1, ldsV0, ldsV1, S0, S1);
-            step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0, S1, S0);
-        }
-        pv(ldsV1, pb);  // P.V(J-1) (with J = 0: zero codes times P = 0)
-        // The rest (masked blocks, and an odd last unmasked one), one at a time.
-        for (int blk = J; blk < nblk; blk++) {
-            __syncthreads();  // every wave is done with K0 and V0
-            fetch(kg, blk, ldsK0, 0);
-            fetch(vg, blk, ldsV0, 1);
-            __syncthreads();
-            qk(ldsK0, S0);
-            softmax_pv(blk, S0, ldsV0);
-        }
-    } else {
-        // Step j: prefetch K(j+1) and V(j+1) into the other buffers, then
-        // QK^T, softmax and P.V of block j; the other waves on the SIMD (three
-        // at this size) fill the MFMA and VALU gaps.
-        auto step = [&](int blk, const uint8_t* k_cur, uint8_t* k_fill, const uint8_t* v_cur, uint8_t* v_fill)
-                        __attribute__((always_inline)) {
-            if (blk + 1 < nblk) {
-                fetch(kg, blk + 1, k_fill, 0);
-                fetch(vg, blk + 1, v_fill, 1);
-            }
-            qk(k_cur, S0);
-            softmax_pv(blk, S0, v_cur);
-            __syncthreads();
-        };
-        fetch(kg, 0, ldsK0, 0);
-        fetch(vg, 0, ldsV0, 1);
-        __syncthreads();
-        for (int blk = 0; blk < nblk; blk += 2) {
-            step(blk, ldsK0, ldsK1, ldsV0, ldsV1);
-            if (blk + 1 < nblk) step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0);
-        }
+    };
+    fetch(kg, 0, ldsK0, 0);
+    fetch(vg, 0, ldsV0, 1);
+    __syncthreads();
+    for (int blk = 0; blk < nblk; blk += 2) {
+        step(blk, ldsK0, ldsK1, ldsV0, ldsV1);
+        if (blk + 1 < nblk) step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0);
     }
 
     // out = O / l * v_scale + v_mean; lane holds channels 32dt + 8j + 4*half + 0..3.
