@@ -35,6 +35,8 @@ class _Problem(C.Structure):
         ("k_sb", C.c_longlong), ("k_st", C.c_longlong), ("k_sh", C.c_longlong),
         ("v_sb", C.c_longlong), ("v_st", C.c_longlong), ("v_sh", C.c_longlong),
         ("q_mul", C.c_float), ("smooth_k", C.c_int), ("smooth_v", C.c_int), ("v_range", C.c_float),
+        ("merge", C.c_int), ("frames", C.c_int), ("special", C.c_int), ("grid_h", C.c_int), ("grid_w", C.c_int),
+        ("dense_frames", C.c_int),
     ]
 
 
@@ -85,10 +87,16 @@ def lib() -> C.CDLL:
         l.oracle_generate.argtypes = [C.POINTER(_GenSpec), vp, vp, vp]
         l.oracle_reference_synthetic.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_uint64, vp, vp, vp]
         l.oracle_prologue.restype = C.c_int
-        l.oracle_prologue.argtypes = [C.POINTER(_Problem), vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int]
+        l.oracle_prologue.argtypes = [C.POINTER(_Problem), vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int]
+        l.oracle_merged_keys.restype = C.c_int
+        l.oracle_merged_keys.argtypes = [C.POINTER(_Problem)]
+        l.oracle_members.restype = C.c_int
+        l.oracle_members.argtypes = [C.POINTER(_Problem), C.c_int, vp]
+        l.oracle_log2_count.restype = C.c_float
+        l.oracle_log2_count.argtypes = [C.c_int]
         l.oracle_attention_f64.argtypes = [C.POINTER(_Problem), C.c_int, C.c_float, vp, vp, vp, vp, C.c_int, vp, C.c_int]
-        l.oracle_sage_emulate.argtypes = [C.POINTER(_Problem), C.c_int, vp, vp, vp, vp, vp, vp, vp, C.c_int, vp, vp,
-                                          C.c_int, C.c_int, C.c_int]
+        l.oracle_sage_emulate.argtypes = [C.POINTER(_Problem), C.c_int, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int, vp,
+                                          vp, C.c_int, C.c_int, C.c_int]
         l.oracle_errors.argtypes = [vp, vp, C.c_size_t, vp]
         _lib = l
     return _lib
@@ -162,6 +170,9 @@ class Problem:
     smooth_v: bool = True
     softmax_scale: float | None = None
     strides: dict = field(default_factory=dict)  # optional {"q": (sb, st, sh), "k": ..., "v": ...}
+    # KV merging (KvMerge::Pool): stride 1 = dense; layout = (frames, special, grid_h, grid_w, dense_frames)
+    merge: int = 1
+    layout: tuple = (1, 0, 0, 0, 0)
 
     @property
     def hk(self) -> int:
@@ -172,8 +183,19 @@ class Problem:
         return -(-self.tokens // QTILE) * QTILE
 
     @property
+    def tk(self) -> int:
+        """Keys after merging (FrameLayout::merged_keys, mod.rs:293-299)."""
+        return lib().oracle_merged_keys(C.byref(self._c()))
+
+    @property
     def tk_pad(self) -> int:
-        return -(-self.tokens // KBLOCK) * KBLOCK
+        return -(-self.tk // KBLOCK) * KBLOCK
+
+    def members(self, j: int) -> list:
+        """Tokens merged key j pools, in member order (reference.rs:79-109)."""
+        buf = (C.c_int * 16)()
+        n = lib().oracle_members(C.byref(self._c()), j, C.cast(buf, C.c_void_p))
+        return list(buf[:n])
 
     def scale(self) -> np.float32:
         if self.softmax_scale is not None:
@@ -191,7 +213,7 @@ class Problem:
         k = self.strides.get("k", dflt(self.hk))
         v = self.strides.get("v", dflt(self.hk))
         return _Problem(self.batch, self.heads, self.hk, t, d, self.dtype, *q, *k, *v, float(self.q_mul()),
-                        int(self.smooth_k), int(self.smooth_v), 448.0)
+                        int(self.smooth_k), int(self.smooth_v), 448.0, int(self.merge), *self.layout)
 
 
 @dataclass
@@ -234,10 +256,12 @@ def prologue(p: Problem, q: np.ndarray, k: np.ndarray, v: np.ndarray, threads: i
         "k_scale": np.zeros((B, HK, p.tk_pad // KBLOCK), np.float32),
         "v8": np.zeros((B, HK, p.tk_pad, D), np.uint8),
         "stats": np.zeros((B, HK, 4, D), np.float32),
+        "kbias": np.zeros((p.tk_pad,), np.float32),
     }
     q, k, v = (np.ascontiguousarray(a, dtype=np.uint16) for a in (q, k, v))
     r = lib().oracle_prologue(C.byref(p._c()), _p(q), _p(k), _p(v), _p(out["q8"]), _p(out["q_scale"]),
-                              _p(out["k8"]), _p(out["k_scale"]), _p(out["v8"]), _p(out["stats"]), threads)
+                              _p(out["k8"]), _p(out["k_scale"]), _p(out["v8"]), _p(out["stats"]), _p(out["kbias"]),
+                              threads)
     if r != 0:
         raise ValueError("oracle prologue: unsupported head dim")
     return out
@@ -269,10 +293,16 @@ def sage_emulate(p: Problem, pro: dict, rows=None, out_dtype: int = BF16, thread
     r, R = _rows(rows, p.tokens)
     out = np.empty((p.batch, p.heads, R, p.head_dim), np.float32)
     o16 = np.empty(out.shape, np.uint16)
+    kb = np.ascontiguousarray(pro.get("kbias", np.zeros(p.tk_pad, np.float32)), dtype=np.float32)
     lib().oracle_sage_emulate(C.byref(p._c()), int(p.causal), _p(pro["q8"]), _p(pro["q_scale"]), _p(pro["k8"]),
-                              _p(pro["k_scale"]), _p(pro["v8"]), _p(pro["stats"]), None if r is None else _p(r), R,
-                              _p(out), _p(o16), out_dtype, int(bool(fast_exp)), threads)
+                              _p(pro["k_scale"]), _p(pro["v8"]), _p(pro["stats"]), _p(kb),
+                              None if r is None else _p(r), R, _p(out), _p(o16), out_dtype, int(bool(fast_exp)), threads)
     return out, o16
+
+
+def log2_count(n: int) -> float:
+    """The KV-merge bias of a key pooling n tokens: log2(n) rounded to f32."""
+    return float(np.float32(lib().oracle_log2_count(n)))
 
 
 def errors(ours: np.ndarray, ref: np.ndarray) -> dict:

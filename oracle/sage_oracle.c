@@ -348,26 +348,96 @@ static void quant_q(const oracle_problem* p, int b, int h, const uint16_t* q, in
     }
 }
 
-/* INT8 K per 64-key block and E4M3 V per channel (sage_quant.cu:259-319):
- * kv = (0 + k) - mean_k; code = RNE clamp(kv * (127/amax_blk)); scale = amax_blk / 127;
- * vq = ((0 + v) - mean_v) * (1/v_scale); code = e4m3 RNE satfinite.
- * Padded keys are 0. Pinned: tolerance invariants tests.rs:538-581, closed forms. */
+/* ------------------------------------------------------------ KV merging */
+
+static int merging(const oracle_problem* p) { return p->merge > 1; }
+
+static int frame_tokens(const oracle_problem* p) { return p->special + p->grid_h * p->grid_w; }
+
+static int merged_per_frame(const oracle_problem* p) {
+    const int s = p->merge;
+    return p->special + ((p->grid_h + s - 1) / s) * ((p->grid_w + s - 1) / s);
+}
+
+/* FrameLayout::merged_keys (mod.rs:293-299). */
+int oracle_merged_keys(const oracle_problem* p) {
+    if (!merging(p)) return p->tokens;
+    const int d = p->dense_frames < p->frames ? p->dense_frames : p->frames;
+    return d * frame_tokens(p) + (p->frames - d) * merged_per_frame(p);
+}
+
+/* reference.rs:79-109 (members, cell_members). Pinned by the reference's
+ * KATs (tests.rs:96-173: the first pooled cell of frame 1, member counts of
+ * edge cells, every token pooled exactly once), ported in tests. */
+int oracle_members(const oracle_problem* p, int j, int* tokens) {
+    if (!merging(p)) {
+        if (tokens) tokens[0] = j;
+        return 1;
+    }
+    const int s = p->merge, ft = frame_tokens(p), per = merged_per_frame(p);
+    const int df = p->dense_frames < p->frames ? p->dense_frames : p->frames;
+    const int dense = df * ft;
+    if (j < dense) {
+        if (tokens) tokens[0] = j;
+        return 1;
+    }
+    const int f = df + (j - dense) / per, loc = (j - dense) % per, base = f * ft;
+    if (loc < p->special) {
+        if (tokens) tokens[0] = base + loc;
+        return 1;
+    }
+    const int cell = loc - p->special, mw = (p->grid_w + s - 1) / s;
+    const int y0 = (cell / mw) * s, x0 = (cell % mw) * s;
+    int n = 0;
+    for (int y = y0; y < y0 + s && y < p->grid_h; y++)
+        for (int x = x0; x < x0 + s && x < p->grid_w; x++) {
+            if (tokens) tokens[n] = base + p->special + y * p->grid_w + x;
+            n++;
+        }
+    return n;
+}
+
+/* log2(n), n = 1..16, each the f32 nearest the exact value (checked in tests
+ * against a 60-digit evaluation and numpy). */
+float oracle_log2_count(int n) {
+    static const uint32_t bits[17] = {0xff800000u, 0x00000000u, 0x3f800000u, 0x3fcae00du, 0x40000000u, 0x40149a78u,
+                                      0x40257007u, 0x4033abb4u, 0x40400000u, 0x404ae00du, 0x40549a78u, 0x405d6754u,
+                                      0x40657007u, 0x406cd401u, 0x4073abb4u, 0x407a0a7fu, 0x40800000u};
+    return (n >= 0 && n <= 16) ? u2f(bits[n]) : (float)log2((double)n);
+}
+
+/* INT8 K per 64-key block and E4M3 V per channel (sage_quant.cu:238-319).
+ * Key j pools its members in order from 0.0f (one member when dense):
+ *   ks = ((0 + k_0) + k_1) + ...,  rc = 1.0f / n,
+ *   kv = fmaf(ks, rc, -mean_k)   code = RNE clamp(kv * (127/amax_blk)), scale = amax_blk / 127,
+ *   vq = fmaf(vs, rc, -mean_v) * (1/v_scale)   code = e4m3 RNE satfinite.
+ * The fused form follows NVRTC's default contraction of `ks * rc - mean`; it
+ * equals the two-rounding form whenever n is a power of two (rc exact), i.e.
+ * for every dense key and every full cell. Padded keys are 0.
+ * Pinned: tolerance invariants tests.rs:538-581 and closed forms in tests;
+ * the fused rounding of 3-, 6-, 9- and 12-member edge cells is unpinned. */
 static void quant_kv(const oracle_problem* p, int b, int hk, const uint16_t* k, const uint16_t* v, const float* st,
                      int8_t* k8, float* ksc, uint8_t* v8) {
-    const int D = p->head_dim, N = p->tokens;
-    const size_t tk_pad = round_up((size_t)N, ORACLE_KBLOCK);
+    const int D = p->head_dim, TK = oracle_merged_keys(p);
+    const size_t tk_pad = round_up((size_t)TK, ORACLE_KBLOCK);
     float* kv = (float*)malloc(sizeof(float) * ORACLE_KBLOCK * D);
+    int mem[16];
     for (size_t blk = 0; blk < tk_pad / ORACLE_KBLOCK; blk++) {
         float amax = 0.f;
         for (int r = 0; r < ORACLE_KBLOCK; r++) {
             int j = (int)(blk * ORACLE_KBLOCK) + r;
+            const int n = j < TK ? oracle_members(p, j, mem) : 0;
+            const float rc = n > 0 ? 1.0f / (float)n : 0.f;
             for (int d = 0; d < D; d++) {
                 float x = 0.f, vq = 0.f;
-                if (j < N) {
-                    float fk = 0.f + dec16(k[b * p->k_sb + (long long)j * p->k_st + hk * p->k_sh + d], p->dtype);
-                    float fv = 0.f + dec16(v[b * p->v_sb + (long long)j * p->v_st + hk * p->v_sh + d], p->dtype);
-                    x = fk - st[d];
-                    vq = (fv - st[D + d]) * st[3 * D + d];
+                if (n > 0) {
+                    float ks = 0.f, vs = 0.f;
+                    for (int m = 0; m < n; m++) {
+                        ks += dec16(k[b * p->k_sb + (long long)mem[m] * p->k_st + hk * p->k_sh + d], p->dtype);
+                        vs += dec16(v[b * p->v_sb + (long long)mem[m] * p->v_st + hk * p->v_sh + d], p->dtype);
+                    }
+                    x = fmaf(ks, rc, -st[d]);
+                    vq = fmaf(vs, rc, -st[D + d]) * st[3 * D + d];
                 }
                 kv[r * D + d] = x;
                 amax = fmaxf(amax, fabsf(x));
@@ -385,11 +455,16 @@ static void quant_kv(const oracle_problem* p, int b, int hk, const uint16_t* k, 
 }
 
 int oracle_prologue(const oracle_problem* p, const uint16_t* q, const uint16_t* k, const uint16_t* v, int8_t* q8,
-                    float* q_scale, int8_t* k8, float* k_scale, uint8_t* v8, float* stats, int threads) {
+                    float* q_scale, int8_t* k8, float* k_scale, uint8_t* v8, float* stats, float* kbias,
+                    int threads) {
     const int D = p->head_dim;
     if (D != 64 && D != 128) return -1;
     const size_t tq_pad = round_up((size_t)p->tokens, ORACLE_QTILE);
-    const size_t tk_pad = round_up((size_t)p->tokens, ORACLE_KBLOCK);
+    const int TK = oracle_merged_keys(p);
+    const size_t tk_pad = round_up((size_t)TK, ORACLE_KBLOCK);
+    if (merging(p) && kbias)
+        for (size_t j = 0; j < tk_pad; j++)
+            kbias[j] = (int)j < TK ? oracle_log2_count(oracle_members(p, (int)j, NULL)) : -INFINITY;
     set_threads(threads);
     const int B = p->batch, H = p->heads, HK = p->kv_heads;
 #pragma omp parallel for schedule(dynamic)
@@ -412,16 +487,42 @@ int oracle_prologue(const oracle_problem* p, const uint16_t* q, const uint16_t* 
 
 /* Softmax attention in f64 (reference.rs:148-184), over the decoded 16-bit
  * inputs; causal rows see keys j <= i; Q head h reads KV head h / (H/HKV).
+ * KV merging pools K and V per (b, kv head) first, as reference.rs:113-143
+ * does (f32 sums in member order, then / n in f32), and adds
+ * log2(n_j) * ln 2 to key j's logits.
  * Pinned: closed forms in tests (uniform keys give the mean of V; one-hot
- * logits select one V row; V = const gives const) and numpy/torch float64. */
+ * logits select one V row; V = const gives const), numpy/torch float64, and
+ * the reference's merged == dense identity on uniform cells (tests.rs:193-232). */
 void oracle_attention_f64(const oracle_problem* p, int causal, float scale, const uint16_t* q, const uint16_t* k,
                           const uint16_t* v, const int* rows, int nrows, float* out, int threads) {
     const int B = p->batch, H = p->heads, HK = p->kv_heads, N = p->tokens, D = p->head_dim, G = H / HK;
+    const int TK = oracle_merged_keys(p);
     const int R = rows ? nrows : N;
+    /* K and V as f32 [b][hk][j][d] over the (possibly merged) keys, and the log-count bias. */
+    float* kf = (float*)malloc(sizeof(float) * (size_t)B * HK * TK * D);
+    float* vf = (float*)malloc(sizeof(float) * (size_t)B * HK * TK * D);
+    double* kb = (double*)malloc(sizeof(double) * (size_t)TK);
+    int mem[16];
+    for (int j = 0; j < TK; j++) {
+        const int n = oracle_members(p, j, mem);
+        kb[j] = merging(p) ? (double)oracle_log2_count(n) * 0.69314718055994530942 : 0.0;
+        for (int b = 0; b < B; b++)
+            for (int hk = 0; hk < HK; hk++)
+                for (int d = 0; d < D; d++) {
+                    float ks = 0.f, vs = 0.f;
+                    for (int m = 0; m < n; m++) {
+                        ks += dec16(k[b * p->k_sb + (long long)mem[m] * p->k_st + hk * p->k_sh + d], p->dtype);
+                        vs += dec16(v[b * p->v_sb + (long long)mem[m] * p->v_st + hk * p->v_sh + d], p->dtype);
+                    }
+                    const size_t o = (((size_t)b * HK + hk) * TK + j) * D + d;
+                    kf[o] = n > 1 ? ks / (float)n : ks;
+                    vf[o] = n > 1 ? vs / (float)n : vs;
+                }
+    }
     set_threads(threads);
 #pragma omp parallel
     {
-        double* logit = (double*)malloc(sizeof(double) * N);
+        double* logit = (double*)malloc(sizeof(double) * TK);
         double* acc = (double*)malloc(sizeof(double) * D);
         double* qi = (double*)malloc(sizeof(double) * D);
 #pragma omp for schedule(dynamic) collapse(2)
@@ -430,13 +531,15 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
                 int b = bh / H, h = bh % H, hk = h / G;
                 int i = rows ? rows[ri] : ri;
                 for (int d = 0; d < D; d++) qi[d] = dec16(q[b * p->q_sb + (long long)i * p->q_st + h * p->q_sh + d], p->dtype);
-                int nk = causal ? i + 1 : N;
+                const float* kr0 = kf + ((size_t)b * HK + hk) * TK * D;
+                const float* vr0 = vf + ((size_t)b * HK + hk) * TK * D;
+                int nk = causal ? i + 1 : TK;
                 double mx = -INFINITY;
                 for (int j = 0; j < nk; j++) {
-                    const uint16_t* kr = k + b * p->k_sb + (long long)j * p->k_st + hk * p->k_sh;
+                    const float* kr = kr0 + (size_t)j * D;
                     double dot = 0;
-                    for (int d = 0; d < D; d++) dot += qi[d] * (double)dec16(kr[d], p->dtype);
-                    logit[j] = dot * (double)scale;
+                    for (int d = 0; d < D; d++) dot += qi[d] * (double)kr[d];
+                    logit[j] = dot * (double)scale + kb[j];
                     if (logit[j] > mx) mx = logit[j];
                 }
                 double sum = 0;
@@ -444,8 +547,8 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
                 for (int j = 0; j < nk; j++) {
                     double pj = exp(logit[j] - mx);
                     sum += pj;
-                    const uint16_t* vr = v + b * p->v_sb + (long long)j * p->v_st + hk * p->v_sh;
-                    for (int d = 0; d < D; d++) acc[d] += pj * (double)dec16(vr[d], p->dtype);
+                    const float* vr = vr0 + (size_t)j * D;
+                    for (int d = 0; d < D; d++) acc[d] += pj * (double)vr[d];
                 }
                 float* o = out + ((size_t)bh * R + ri) * D;
                 for (int d = 0; d < D; d++) o[d] = (float)(acc[d] / sum);
@@ -454,6 +557,9 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
         free(acc);
         free(qi);
     }
+    free(kf);
+    free(vf);
+    free(kb);
 }
 
 /* Correctly rounded exp2 in f32 (the build's stand-in for a hardware exp2;
@@ -479,11 +585,12 @@ static inline float ex2f_cr(float x) { return (float)exp2((double)x); }
  * within the quantisation error; sequential sums replace the GPU's lane order. */
 void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, const float* q_scale,
                          const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* stats,
-                         const int* rows, int nrows, float* out, uint16_t* out16, int out_dtype, int fast_exp,
-                         int threads) {
+                         const float* kbias, const int* rows, int nrows, float* out, uint16_t* out16, int out_dtype,
+                         int fast_exp, int threads) {
     const int B = p->batch, H = p->heads, HK = p->kv_heads, N = p->tokens, D = p->head_dim, G = H / HK;
     const float kMagic = 12582912.0f; /* 1.5 * 2^23 */
-    const size_t tq_pad = round_up((size_t)N, ORACLE_QTILE), tk_pad = round_up((size_t)N, ORACLE_KBLOCK);
+    const int TK = oracle_merged_keys(p), merged = merging(p);
+    const size_t tq_pad = round_up((size_t)N, ORACLE_QTILE), tk_pad = round_up((size_t)TK, ORACLE_KBLOCK);
     const int nblk = (int)(tk_pad / ORACLE_KBLOCK);
     const int R = rows ? nrows : N;
     const float kLog448 = 8.807354922057604f;
@@ -514,7 +621,7 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
                     int32_t smax = 0;
                     for (int r = 0; r < ORACLE_KBLOCK; r++) {
                         int j = blk * ORACLE_KBLOCK + r;
-                        int ok = j < N && (!causal || j <= i);
+                        int ok = j < TK && (!causal || j <= i);
                         int32_t s = 0;
                         if (ok) {
                             const int8_t* kj = kb + (size_t)j * D;
@@ -527,14 +634,32 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
                     /* x as the reference holds it: exact, or biased by kMagic (both exact floats) */
                     const float bias = fast_exp ? kMagic : 0.f;
                     const float xoff = fast_exp ? -kMagic * sc : 0.f;
-                    float mnew = m;
-                    if (have) mnew = fmaxf(m, fmaf(bias + (float)smax, sc, xoff));
+                    float mnew = m, off;
+                    float X[ORACLE_KBLOCK];
+                    if (merged) {
+                        /* the log2 logit with the log-count bias; padding keys carry -inf */
+                        float mx = -INFINITY;
+                        for (int r = 0; r < ORACLE_KBLOCK; r++) {
+                            const int j = blk * ORACLE_KBLOCK + r;
+                            const float kb = kbias[j];
+                            const float bo = fast_exp ? fmaf(-kMagic, sc, kb) : kb;
+                            X[r] = S[r] == INT32_MIN ? -INFINITY : fmaf(bias + (float)S[r], sc, bo);
+                            mx = fmaxf(mx, X[r]);
+                        }
+                        mnew = fmaxf(m, mx);
+                        off = kLog448 - mnew;
+                    } else {
+                        if (have) mnew = fmaxf(m, fmaf(bias + (float)smax, sc, xoff));
+                        off = (kLog448 - mnew) + xoff;
+                    }
                     const float alpha = ex2f_cr(m - mnew);
                     m = mnew;
-                    const float off = (kLog448 - mnew) + xoff;
                     float sum = 0.f;
                     for (int r = 0; r < ORACLE_KBLOCK; r++) {
-                        float pr = S[r] == INT32_MIN ? 0.f : ex2f_cr(fmaf(bias + (float)S[r], sc, off));
+                        float pr;
+                        if (S[r] == INT32_MIN) pr = 0.f;
+                        else if (merged) pr = ex2f_cr(X[r] + off);
+                        else pr = ex2f_cr(fmaf(bias + (float)S[r], sc, off));
                         P[r] = pr;
                         sum += pr;
                     }

@@ -48,7 +48,23 @@ typedef struct {
     int smooth_k;  /* subtract the per-channel K mean */
     int smooth_v;  /* subtract the per-channel V mean (added back at the end) */
     float v_range; /* 448 */
+    /* KV merging (mod.rs:270-311, KvMerge::Pool): merge = 1 is dense; 2 or 4
+     * pools each frame's grid_h x grid_w patch grid in merge x merge cells,
+     * keeping the `special` tokens of every frame and every token of the
+     * first `dense_frames` frames. */
+    int merge;
+    int frames, special, grid_h, grid_w, dense_frames;
 } oracle_problem;
+
+/* Keys after merging (FrameLayout::merged_keys, mod.rs:293-299); tokens when dense. */
+int oracle_merged_keys(const oracle_problem* p);
+/* Tokens merged key j pools, in the reference's member order (row-major in
+ * the cell; reference.rs:79-109, sage_quant.cu:210-235); returns the count
+ * (<= 16) and writes the tokens to `tokens` (may be NULL). */
+int oracle_members(const oracle_problem* p, int j, int* tokens);
+/* log2(n) for n = 1..16, correctly rounded to f32: the KV-merge bias of a key
+ * that pools n tokens (sage_quant.cu:321-325). */
+float oracle_log2_count(int n);
 
 /* ---- codecs ---- */
 float oracle_bf16_to_f32(uint16_t b);
@@ -97,17 +113,22 @@ void oracle_reference_synthetic(int batch, int tokens, int heads, int d, uint64_
  *   k8      [b][hkv][tk_pad][D]      k_scale [b][hkv][tk_pad/64]
  *   v8      [b][hkv][tk_pad][D]  E4M3 codes, keys in natural order
  *   stats   [b][hkv][4][D]           K mean, V mean, V scale, 1/V scale
+ *   kbias   [tk_pad]                 merged: log2(member count), -inf past tk;
+ *                                    dense: left untouched (may be NULL)
+ * k8/k_scale/v8 cover the merged keys (tk_pad = merged keys rounded to 64).
  * Returns 0, or -1 for an unsupported head dim. */
 int oracle_prologue(const oracle_problem* p, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                     int8_t* q8, float* q_scale, int8_t* k8, float* k_scale, uint8_t* v8, float* stats,
-                    int threads);
+                    float* kbias, int threads);
 
 /* ---- attention ----
  * `rows` (nrows entries, each < tokens) selects the query rows computed for
  * every (b, h); NULL computes all rows. Output layout [b][h][nrows][D]. */
 
 /* Textbook softmax attention in f64 of the 16-bit inputs (reference.rs:148-184),
- * with causal masking and grouped-query heads. */
+ * with causal masking and grouped-query heads. With KV merging, K and V are
+ * pooled as reference.rs:113-143 does (f32 sums in member order, then / n)
+ * and key j's logit gains log2(n_j) * ln 2. */
 void oracle_attention_f64(const oracle_problem* p, int causal, float scale, const uint16_t* q,
                           const uint16_t* k, const uint16_t* v, const int* rows, int nrows, float* out,
                           int threads);
@@ -120,10 +141,14 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
  * fast_exp = 1 is the reference's default logit arithmetic (SG_FAST_EXP=1:
  * scores biased by 1.5 * 2^23, the bias removed inside the exp2 FMA);
  * fast_exp = 0 converts the int32 scores exactly (SG_FAST_EXP=0). */
+/* With KV merging (kbias from oracle_prologue), the merged kernel's logit
+ * arithmetic (sage_attn.cu:264-305 with MERGE): x = fmaf(S', sc, b') with
+ * S' = 1.5*2^23 + S and b' = fmaf(-1.5*2^23, sc, kbias) (fast_exp = 1) or
+ * S' = S, b' = kbias (fast_exp = 0); m = max(m, max x); p = 2^(x + (log2(448) - m)). */
 void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, const float* q_scale,
                          const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* stats,
-                         const int* rows, int nrows, float* out, uint16_t* out16, int out_dtype,
-                         int fast_exp, int threads);
+                         const float* kbias, const int* rows, int nrows, float* out, uint16_t* out16,
+                         int out_dtype, int fast_exp, int threads);
 
 /* Errors of `ours` against `ref` (reference.rs:202-225):
  * out[0] cos, [1] rel_l1, [2] rel_l2, [3] max_abs, [4] ref_max. */

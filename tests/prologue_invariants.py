@@ -3,15 +3,35 @@ platform/spl-nn/src/sage/tests.rs:476-594, check_prologue), as tolerance
 invariants over logical-layout buffers: Q scale within 1e-4 of amax/127*q_mul
 and every Q code within half a step; K mean within 1e-3 of the f64 mean; K
 scale within 1e-4 of amax/127 and every K code within half a step; V
-de-quantised within |v - mean|/16 + scale * 2^-8. Dense plans (no KV merge)."""
+de-quantised within |v - mean|/16 + scale * 2^-8. With KV merging the keys are
+the reference's pooled K and V (reference.rs:113-143: f32 sums in member order,
+then / n) and every kbias entry is log2(n) within 1e-6, -inf past the keys."""
 from __future__ import annotations
 
 import numpy as np
 
 
+def pool_kv(p, kk: np.ndarray, vv: np.ndarray):
+    """reference.rs:113-143 for one (batch, head): [T,D] -> pooled [tk,D] K and V, member counts."""
+    tk = p.tk
+    km = np.zeros((tk, kk.shape[1]), np.float32)
+    vm = np.zeros_like(km)
+    n = np.zeros(tk, np.int64)
+    for j in range(tk):
+        mem = p.members(j)
+        for t in mem:
+            km[j] += kk[t]
+            vm[j] += vv[t]
+        km[j] /= np.float32(len(mem))
+        vm[j] /= np.float32(len(mem))
+        n[j] = len(mem)
+    return km, vm, n
+
+
 def check_prologue(p, qf: np.ndarray, kf: np.ndarray, vf: np.ndarray, pro: dict, smooth: bool = True) -> None:
     """qf, kf, vf: decoded inputs [B,T,H,D] / [B,T,HKV,D] float32."""
     B, T, H, HK, D = p.batch, p.tokens, p.heads, p.hk, p.head_dim
+    TK = p.tk
     qmul = np.float32(np.float32(1.4426950408889634) / np.sqrt(np.float32(D))) if p.softmax_scale is None \
         else np.float32(np.float32(p.softmax_scale) * np.float32(1.4426950408889634))
     tq, tk = p.tq_pad, p.tk_pad
@@ -35,8 +55,9 @@ def check_prologue(p, qf: np.ndarray, kf: np.ndarray, vf: np.ndarray, pro: dict,
                 assert np.all(np.abs(st[0].astype(np.float64) - m) < 1e-3 * (1.0 + np.abs(m))), "k mean"
             else:
                 assert np.all(st[:2] == 0.0), "means must be 0 without smoothing"
+            km, vm, _ = pool_kv(p, kk, vf[b, :, h]) if p.merge > 1 else (kk, vf[b, :, h], None)
             ks = np.zeros((tk, D), np.float32)
-            ks[:T] = kk - st[0]
+            ks[:TK] = km - st[0]
             blocks = ks.reshape(tk // 64, 64, D)
             amax = np.abs(blocks).max(axis=(1, 2))
             got = pro["k_scale"][b, h]
@@ -46,10 +67,18 @@ def check_prologue(p, qf: np.ndarray, kf: np.ndarray, vf: np.ndarray, pro: dict,
                 "k codes"
             from oracle import pyoracle
 
-            vdq = pyoracle.e4m3_decode(pro["v8"][b, h, :T]) * st[2] + st[1]
-            want = vf[b, :, h]
+            vdq = pyoracle.e4m3_decode(pro["v8"][b, h, :TK]) * st[2] + st[1]
+            want = vm
             tol = np.abs(want - st[1]) / 16.0 + st[2] * 2.0 ** -8
             assert np.all(np.abs(vdq - want) <= tol * 1.01), "v codes"
-            assert np.all(pro["v8"][b, h, T:] == 0) and np.all(pro["k8"][b, h, T:] == 0), "padding keys"
+            assert np.all(pro["v8"][b, h, TK:] == 0) and np.all(pro["k8"][b, h, TK:] == 0), "padding keys"
         for h in range(H):
             assert np.all(pro["q8"][b, h, T:] == 0), "padding queries"
+    if p.merge > 1:
+        kb = pro["kbias"]
+        for j in range(tk):
+            if j < TK:
+                want = np.log2(np.float32(len(p.members(j))))
+                assert abs(float(kb[j]) - float(want)) <= 1e-6, ("bias", j, kb[j], want)
+            else:
+                assert kb[j] == -np.inf, ("padding bias", j)
