@@ -90,8 +90,10 @@ typedef struct sage_frame_layout {
 } sage_frame_layout;
 
 /* KvMerge (mod.rs:302-311): stride 1 = Dense, 2 or 4 = Pool{stride, layout}.
- * Plans are computed for every variant; prepare/attend of a pooled plan
- * return SAGE_ERR_UNSUPPORTED in this build. */
+ * A pooled plan averages K and V over stride x stride patch cells of every
+ * frame past the first `dense_frames` (special tokens stay single) and gives
+ * each key a log2(member count) logit bias; queries are never merged. Causal
+ * masking (an extension) is refused over merged keys (SAGE_ERR_UNSUPPORTED). */
 typedef struct sage_kv_merge {
     uint32_t stride;
     sage_frame_layout layout;
@@ -152,7 +154,8 @@ typedef struct sage_options {
  *   v8      u8  [b][g][tk_pad/64][D][64]   E4M3, key k of a block at byte
  *                                          sage_v8_position(k) of its row
  *   stats   f32 [b][g][4][D]               K mean, V mean, V scale, 1/V scale
- *   kbias   f32 [tk_pad]                   KV-merge bias (unused when dense) */
+ *   kbias   f32 [tk_pad]                   KV-merge bias: log2(member count),
+ *                                          -inf past tk (unused when dense) */
 typedef struct sage_ws_buffers {
     int8_t* q8;
     float* q_scale;

@@ -275,8 +275,6 @@ sage_status sage_workspace_new(const sage_attention* s, const sage_shape* shape,
     sage_plan plan;
     sage_status st = sage_plan_new(shape, merge ? merge : &dense, &plan);
     if (st != SAGE_OK) return st;
-    if (plan.merge.stride != 1)
-        return fail(SAGE_ERR_UNSUPPORTED, "KV merging (KvMerge::Pool) is not supported by this build");
     const uint64_t b = plan.shape.batch, h = plan.shape.heads, hk = plan.shape.kv_heads, d = s->head_dim;
     sage_workspace* w = new sage_workspace;
     w->plan = plan;
@@ -387,6 +385,10 @@ sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage
                         (u64)(4 * d));
         return fail(SAGE_ERR_UNSUPPORTED, "the fused QK LayerNorm (QkNorm) is not supported by this build");
     }
+    // Causal masking (an extension) is defined over token positions; merged
+    // keys have none.
+    if (opts->causal && plan.merge.stride != 1)
+        return fail(SAGE_ERR_UNSUPPORTED, "causal masking over merged keys (KvMerge::Pool) is not supported");
     int flags = 0;
     if (opts->smooth_k) flags |= sage::F_SMOOTH_K;
     if (opts->smooth_v) flags |= sage::F_SMOOTH_V;
@@ -418,8 +420,22 @@ sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage
     g.flags = flags;
     g.q_mul = scale * log2e;
     g.v_range = SAGE_FP8_MAX;
+    // Merge geometry (mod.rs:727-770): a dense plan is one frame of `tokens`
+    // tokens with merge = 1.
+    const sage_frame_layout& l = plan.merge.layout;
+    const uint64_t ms = plan.merge.stride;
+    g.merge = (int)ms;
+    if (ms > 1) {
+        g.frame_tokens = (int)tokens_per_frame(l);
+        g.special = (int)l.special;
+        g.grid_h = (int)l.grid_h;
+        g.grid_w = (int)l.grid_w;
+        g.merged_frame = (int)merged_per_frame(l, ms);
+        g.merged_w = (int)((l.grid_w + ms - 1) / ms);
+        g.dense_frames = (int)(l.dense_frames < l.frames ? l.dense_frames : l.frames);
+    }
 
-    sage::PrologueBufs bufs{ws->q8, ws->q_scale, ws->k8, ws->k_scale, ws->v8, ws->stats, ws->part};
+    sage::PrologueBufs bufs{ws->q8, ws->q_scale, ws->k8, ws->k_scale, ws->v8, ws->stats, ws->part, ws->kbias};
     hipError_t e = sage::launch_prologue((int)d, static_cast<const uint16_t*>(q->data),
                                          static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
                                          bufs, g, s->stream);
@@ -445,7 +461,7 @@ sage_status sage_attend(const sage_attention* s, const sage_workspace* ws, const
     g.o_st = (long long)out->strides.token;
     g.o_sh = (long long)out->strides.head;
     g.flags = (g.flags & ~sage::F_OUT_F16) | (out->dtype == SAGE_F16 ? sage::F_OUT_F16 : 0);
-    sage::AttendBufs bufs{ws->q8, ws->q_scale, ws->k8, ws->k_scale, ws->v8, ws->stats, out->data};
+    sage::AttendBufs bufs{ws->q8, ws->q_scale, ws->k8, ws->k_scale, ws->v8, ws->stats, ws->kbias, out->data};
     hipError_t e = sage::launch_attention((int)s->head_dim, bufs, g, s->stream);
     if (e != hipSuccess) return hip_fail(e, "launch sage attention");
     return ok();

@@ -40,6 +40,11 @@
 //   Q^T operands wait in LDS to make room), four at head dim 64.
 // - Workgroups are dealt to XCDs so that the ones sharing a head's K and V
 //   share an L2.
+// - KV merging (MERGE, the reference's sg_attn_merge, sage_attn.cu:238-246,
+//   264-305): every key carries a log2(member count) bias, staged per block
+//   in LDS beside K and V. The log2 logit x = S * sc + bias is formed before
+//   the row max (fmaf(1.5 * 2^23 + S, sc, fmaf(-1.5 * 2^23, sc, bias))), and
+//   P = 2^(x + log2(448) - m); padding keys carry -inf and need no mask.
 #include "sage_device.hpp"
 #include "sage_internal.hpp"
 
@@ -95,12 +100,14 @@ __device__ __forceinline__ bool half_selector(int lane) {
     return (int)__builtin_amdgcn_permlane32_swap(lane, lane, false, false)[0] != lane;
 }
 
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 3) void sage_attn(const int8_t* __restrict__ q8, const float* __restrict__ q_scale,
+// The merged head-dim-128 kernel needs the registers of two waves a SIMD.
+template <int D, bool CAUSAL, bool MERGE>
+__global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(const int8_t* __restrict__ q8, const float* __restrict__ q_scale,
                                                     const int8_t* __restrict__ k8,
                                                     const float* __restrict__ k_scale,
                                                     const uint8_t* __restrict__ v8, const float* __restrict__ stats,
-                                                    uint16_t* __restrict__ out, Geom g) {
+                                                    const float* __restrict__ kbias, uint16_t* __restrict__ out,
+                                                    Geom g) {
     constexpr int BN = ATTN_BN;
     // Head dim 128 keeps its Q^T operands in LDS (three waves a SIMD fit in
     // the registers then); head dim 64 keeps them in registers (four waves).
@@ -122,6 +129,9 @@ __global__ __launch_bounds__(256, 3) void sage_attn(const int8_t* __restrict__ q
     __shared__ __attribute__((aligned(16))) uint8_t ldsV1[TILE];
     // Q^T operands, [wave][k-step][lane] (head dim 128 only).
     __shared__ v4i ldsQ[Q_IN_LDS ? 4 : 1][KS][64];
+    // Merge biases of the current and the next block.
+    __shared__ __attribute__((aligned(16))) float ldsB0[MERGE ? BN : 4];
+    __shared__ __attribute__((aligned(16))) float ldsB1[MERGE ? BN : 4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 31, half = lane >> 5;
     const int ntq = gridDim.x;
@@ -156,8 +166,9 @@ __global__ __launch_bounds__(256, 3) void sage_attn(const int8_t* __restrict__ q
     int nblk = g.kblocks;
     if (CAUSAL) nblk = min(nblk, (qt * ATTN_ROWS + ATTN_ROWS - 1) / BN + 1);
     // Leading blocks no query of the workgroup needs masked: every key exists
-    // and (causal) precedes the workgroup's first query.
-    int nfull = min(nblk, g.tk / BN);
+    // and (causal) precedes the workgroup's first query. Merged padding keys
+    // carry a -inf bias instead.
+    int nfull = MERGE ? nblk : min(nblk, g.tk / BN);
     if (CAUSAL) nfull = min(nfull, (qt * ATTN_ROWS + 1) / BN);
 
     const uint8_t* kg = reinterpret_cast<const uint8_t*>(k8) + bhk * (long long)g.tk_pad * D;
@@ -178,6 +189,12 @@ __global__ __launch_bounds__(256, 3) void sage_attn(const int8_t* __restrict__ q
         foff[i][0] = 16u * (uint32_t)swz(i * 256 + wv * 64 + lane, KCPR);
         foff[i][1] = 16u * (uint32_t)swz(i * 256 + wv * 64 + lane, 4);
     }
+    // The 64 merge biases of block blk: one dword a lane of wave 0.
+    auto fetch_bias = [&](int blk, float* dst) __attribute__((always_inline)) {
+        if (MERGE && wv == 0)
+            __builtin_amdgcn_global_load_lds(kbias + blk * BN + lane, (__attribute__((address_space(3))) void*)dst, 4,
+                                             0, 0);
+    };
     auto fetch = [&](const uint8_t* src_base, int blk, uint8_t* dst, int which) __attribute__((always_inline)) {
         const uint8_t* tb = opaque_uniform(src_base + (long long)blk * TILE);
 #pragma unroll
@@ -239,12 +256,59 @@ __global__ __launch_bounds__(256, 3) void sage_attn(const int8_t* __restrict__ q
     // Softmax of block blk (scores sc, biased by 1.5 * 2^23): updates m and l,
     // writes the P^T operand into pn and returns alpha = 2^(m_old - m_new);
     // grow says whether this row's max moved.
-    auto softmax = [&](int blk, v16i (&sc)[2], bool masked, v8i& pn, bool& grow) __attribute__((always_inline)) {
+    auto softmax = [&](int blk, v16i (&sc)[2], bool masked, v8i& pn, bool& grow, const float* bias)
+                       __attribute__((always_inline)) {
         // The reference's fp32 operation order for the logits: no FMA contraction.
 #pragma clang fp contract(off)
         // q_scale * k_scale, kept above zero so that -inf * scl stays -inf.
         const float scl = fmaxf(qs * ksc[blk], 1.0e-30f);
         const float xoff = -MAGIC * scl;
+        if constexpr (MERGE) {
+            // Element (t, r) is key 32t + 8(r >> 2) + 4 half + (r & 3): four
+            // consecutive keys a 16-byte bias read.
+            float x[32];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float4 bb = *reinterpret_cast<const float4*>(bias + 32 * t + 8 * j + 4 * half);
+                    const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int r = 4 * j + i;
+                        x[16 * t + r] = fmaf(__int_as_float(sc[t][r]), scl, fmaf(-MAGIC, scl, bv[i]));
+                    }
+                }
+            float mx = x[0];
+#pragma unroll
+            for (int e = 1; e < 32; e++) mx = fmaxf(mx, x[e]);
+            mx = fmaxf(mx, swap_halves(mx, sel));
+            const float mnew = fmaxf(m, mx);
+            grow = mnew > m;
+            const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+            m = mnew;
+            const float off = LOG2_448 - mnew;
+            float p[2][16];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) p[t][r] = __builtin_amdgcn_exp2f(x[16 * t + r] + off);
+            float q16[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) q16[r] = p[0][r] + p[1][r];
+#pragma unroll
+            for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+                for (int r = 0; r < w; r++) q16[r] += q16[r + w];
+            l = fmaf(l, alpha, q16[0]);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int t = j >> 2, r0 = 4 * (j & 3);
+                const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0], p[t][r0 + 1], pn[j], false);
+                pn[j] = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0 + 2], p[t][r0 + 3], lo, true);
+            }
+            return alpha;
+        }
         if (masked) {
             // Keys past the sequence, and keys after the query when causal. Element
             // (t, r) is key blk*BN + 4*half + c with the constant c below, so one
@@ -334,9 +398,10 @@ __global__ __launch_bounds__(256, 3) void sage_attn(const int8_t* __restrict__ q
         }
     };
     // One whole block, unpipelined: softmax, rescale, P.V.
-    auto softmax_pv = [&](int blk, v16i (&sc)[2], const uint8_t* v_cur) __attribute__((always_inline)) {
+    auto softmax_pv = [&](int blk, v16i (&sc)[2], const uint8_t* v_cur, const float* b_cur)
+                          __attribute__((always_inline)) {
         bool grow;
-        const float alpha = softmax(blk, sc, blk >= nfull, pb, grow);
+        const float alpha = softmax(blk, sc, blk >= nfull, pb, grow, b_cur);
         __builtin_amdgcn_sched_barrier(0);
         rescale(alpha, grow);
         pv(v_cur, pb);
@@ -346,22 +411,24 @@ __global__ __launch_bounds__(256, 3) void sage_attn(const int8_t* __restrict__ q
     // Step j: prefetch K(j+1) and V(j+1) into the other buffers, then
     // QK^T, softmax and P.V of block j; the other waves on the SIMD fill the
     // MFMA and VALU gaps.
-    auto step = [&](int blk, const uint8_t* k_cur, uint8_t* k_fill, const uint8_t* v_cur, uint8_t* v_fill)
-                    __attribute__((always_inline)) {
+    auto step = [&](int blk, const uint8_t* k_cur, uint8_t* k_fill, const uint8_t* v_cur, uint8_t* v_fill,
+                    const float* b_cur, float* b_fill) __attribute__((always_inline)) {
         if (blk + 1 < nblk) {
             fetch(kg, blk + 1, k_fill, 0);
             fetch(vg, blk + 1, v_fill, 1);
+            fetch_bias(blk + 1, b_fill);
         }
         qk(k_cur, S0);
-        softmax_pv(blk, S0, v_cur);
+        softmax_pv(blk, S0, v_cur, b_cur);
         __syncthreads();
     };
     fetch(kg, 0, ldsK0, 0);
     fetch(vg, 0, ldsV0, 1);
+    fetch_bias(0, ldsB0);
     __syncthreads();
     for (int blk = 0; blk < nblk; blk += 2) {
-        step(blk, ldsK0, ldsK1, ldsV0, ldsV1);
-        if (blk + 1 < nblk) step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0);
+        step(blk, ldsK0, ldsK1, ldsV0, ldsV1, ldsB0, ldsB1);
+        if (blk + 1 < nblk) step(blk + 1, ldsK1, ldsK0, ldsV1, ldsV0, ldsB1, ldsB0);
     }
 
     // out = O / l * v_scale + v_mean; lane holds channels 32dt + 8j + 4*half + 0..3.
@@ -391,27 +458,34 @@ __global__ __launch_bounds__(256, 3) void sage_attn(const int8_t* __restrict__ q
     }
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool MERGE>
 static hipError_t launch_d(const AttendBufs& w, const Geom& g, hipStream_t s) {
-    hipLaunchKernelGGL((sage_attn<D, CAUSAL>), dim3(g.tq_pad / ATTN_ROWS, g.heads, g.batch), dim3(256), 0, s, w.q8,
-                       w.q_scale, w.k8, w.k_scale, w.v8, w.stats, static_cast<uint16_t*>(w.out), g);
+    hipLaunchKernelGGL((sage_attn<D, CAUSAL, MERGE>), dim3(g.tq_pad / ATTN_ROWS, g.heads, g.batch), dim3(256), 0, s,
+                       w.q8, w.q_scale, w.k8, w.k_scale, w.v8, w.stats, w.kbias, static_cast<uint16_t*>(w.out), g);
     return hipGetLastError();
 }
 
+// Dense, causal (an extension) or merged (sg_attn_merge); the API refuses
+// causal masking over merged keys.
+template <int D>
+static hipError_t launch_dim(const AttendBufs& w, const Geom& g, hipStream_t s) {
+    if (g.merge > 1) return launch_d<D, false, true>(w, g, s);
+    return (g.flags & F_CAUSAL) ? launch_d<D, true, false>(w, g, s) : launch_d<D, false, false>(w, g, s);
+}
+
 hipError_t launch_attention(int head_dim, const AttendBufs& w, const Geom& g, hipStream_t s) {
-    const bool causal = g.flags & F_CAUSAL;
-    if (head_dim == 64) return causal ? launch_d<64, true>(w, g, s) : launch_d<64, false>(w, g, s);
-    return causal ? launch_d<128, true>(w, g, s) : launch_d<128, false>(w, g, s);
+    return head_dim == 64 ? launch_dim<64>(w, g, s) : launch_dim<128>(w, g, s);
 }
 
 hipError_t attention_resources(int head_dim, bool causal, int* regs, int* spill, int* lds) {
     hipFuncAttributes a;
     const void* f;
     if (head_dim == 64)
-        f = causal ? reinterpret_cast<const void*>(&sage_attn<64, true>) : reinterpret_cast<const void*>(&sage_attn<64, false>);
+        f = causal ? reinterpret_cast<const void*>(&sage_attn<64, true, false>)
+                   : reinterpret_cast<const void*>(&sage_attn<64, false, false>);
     else
-        f = causal ? reinterpret_cast<const void*>(&sage_attn<128, true>)
-                   : reinterpret_cast<const void*>(&sage_attn<128, false>);
+        f = causal ? reinterpret_cast<const void*>(&sage_attn<128, true, false>)
+                   : reinterpret_cast<const void*>(&sage_attn<128, false, false>);
     hipError_t e = hipFuncGetAttributes(&a, f);
     if (e != hipSuccess) return e;
     *regs = a.numRegs;

@@ -35,7 +35,42 @@ struct Geom {
     int flags;
     float q_mul;    // softmax scale * log2(e), folded into the Q scales
     float v_range;  // max |V - mean| maps to this E4M3 value (448)
+    // KV merging (the reference's SgGeom merge fields, sage_common.cu:39-64):
+    // merge = 1 is dense; 2 or 4 pools each frame's grid_h x grid_w patch
+    // grid in merge x merge cells (merged_w cells a row, merged_frame keys a
+    // frame), keeping the `special` tokens and the first dense_frames frames.
+    int merge, frame_tokens, special, grid_h, grid_w, merged_frame, merged_w, dense_frames;
 };
+
+// Members of merged key j (sage_quant.cu:210-235): returns the count; member
+// m (0 <= m < count) is token base + (m / nx) * grid_w + m % nx.
+__device__ __forceinline__ int merged_members(const Geom& g, int j, int& base, int& nx) {
+    nx = 1;
+    base = j;
+    if (g.merge == 1) return 1;
+    const int dense = g.dense_frames * g.frame_tokens;
+    if (j < dense) return 1;
+    const int f = g.dense_frames + (j - dense) / g.merged_frame, loc = (j - dense) % g.merged_frame;
+    if (loc < g.special) {
+        base = f * g.frame_tokens + loc;
+        return 1;
+    }
+    const int cell = loc - g.special;
+    const int y0 = (cell / g.merged_w) * g.merge, x0 = (cell % g.merged_w) * g.merge;
+    const int ny = min(g.merge, g.grid_h - y0);
+    nx = min(g.merge, g.grid_w - x0);
+    base = f * g.frame_tokens + g.special + y0 * g.grid_w + x0;
+    return ny * nx;
+}
+
+// log2(n) for n = 1..16, each the f32 nearest the exact value: the KV-merge
+// bias of a key that pools n tokens (n <= 16 for strides 2 and 4).
+__device__ __forceinline__ float log2_count(int n) {
+    constexpr uint32_t bits[17] = {0xff800000u, 0x00000000u, 0x3f800000u, 0x3fcae00du, 0x40000000u, 0x40149a78u,
+                                   0x40257007u, 0x4033abb4u, 0x40400000u, 0x404ae00du, 0x40549a78u, 0x405d6754u,
+                                   0x40657007u, 0x406cd401u, 0x4073abb4u, 0x407a0a7fu, 0x40800000u};
+    return __uint_as_float(bits[n]);
+}
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));

@@ -17,6 +17,7 @@ struct PrologueBufs {
     uint8_t* v8;
     float* stats;
     float* part;
+    float* kbias;  // [tk_pad]: log2 member count of each merged key, -inf past tk (merged plans)
 };
 
 // The attention kernel's inputs.
@@ -27,6 +28,7 @@ struct AttendBufs {
     const float* k_scale;
     const uint8_t* v8;
     const float* stats;
+    const float* kbias;  // merged plans only
     void* out;
 };
 

@@ -7,7 +7,9 @@
 //                  INT8 Q of the `group` query heads that share the KV head
 //   sage_finalize  grid (kv_heads, batch): K mean, V mean, V scale, 1/V scale
 //   sage_quant_kv  grid (kblocks, kv_heads, batch): smoothed INT8 K and FP8 V,
-//                  V transposed per 64-key block into the MFMA operand order
+//                  V transposed per 64-key block into the MFMA operand order;
+//                  with KV merging each key pools its members (and the keys'
+//                  log2 member counts go to kbias)
 //
 // Codes and scales are bit-identical to the reference's
 // (sezer-muhammed/sota-papers-lab, platform/spl-nn/cuda/sage_quant.cu:59-206,
@@ -211,12 +213,16 @@ __global__ __launch_bounds__(4 * D) void sage_finalize(const float* __restrict__
     }
 }
 
-// sage_quant.cu:238-319 (sg_quant_kv), dense: K - mean -> INT8 per block,
+// sage_quant.cu:238-319 (sg_quant_kv): K - mean -> INT8 per block,
 // (V - mean) / scale -> E4M3, V stored [block][channel][v8_position(key)].
+// A merged key sums its members in order from 0.0f and takes
+// fmaf(sum, 1/n, -mean): NVRTC's default contraction of the reference's
+// `sum * rc - mean`, equal to the dense (k + 0) - mean when n = 1.
 template <int D>
 __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                      const float* __restrict__ stats, int8_t* __restrict__ k8,
-                                                     float* __restrict__ k_scale, uint8_t* __restrict__ v8, Geom g) {
+                                                     float* __restrict__ k_scale, uint8_t* __restrict__ v8,
+                                                     float* __restrict__ kbias, Geom g) {
     constexpr int CH = D / 8;
     constexpr int TPI = 256 / CH;
     constexpr int NI = KBLOCK / TPI;
@@ -237,32 +243,71 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
         mv[e] = st[D + ch * 8 + e];
         iv[e] = st[3 * D + ch * 8 + e];
     }
-    uint4 kraw[NI], vraw[NI];
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-        const int j = blk * KBLOCK + slot + i * TPI;
-        const bool ok = j < g.tk;
-        kraw[i] = load16(k + b * g.k_sb + (long long)j * g.k_st + hk * g.k_sh + ch * 8, ok);
-        vraw[i] = load16(v + b * g.v_sb + (long long)j * g.v_st + hk * g.v_sh + ch * 8, ok);
-    }
-    __syncthreads();
     float kv[NI][8];
     float amax = 0.f;
+    if (g.merge == 1) {
+        uint4 kraw[NI], vraw[NI];
 #pragma unroll
-    for (int i = 0; i < NI; i++) {
-        const int kl = slot + i * TPI;
-        const bool ok = blk * KBLOCK + kl < g.tk;
-        float fk[8], fv[8];
-        unpack8(kraw[i], fk, f16);
-        unpack8(vraw[i], fv, f16);
-        const int pos = v8_position(kl);
+        for (int i = 0; i < NI; i++) {
+            const int j = blk * KBLOCK + slot + i * TPI;
+            const bool ok = j < g.tk;
+            kraw[i] = load16(k + b * g.k_sb + (long long)j * g.k_st + hk * g.k_sh + ch * 8, ok);
+            vraw[i] = load16(v + b * g.v_sb + (long long)j * g.v_st + hk * g.v_sh + ch * 8, ok);
+        }
+        __syncthreads();
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            // The reference sums the (one) member from 0.0f first: -0 becomes +0.
-            kv[i][e] = ok ? (fk[e] + 0.0f) - mk[e] : 0.f;
-            amax = fmaxf(amax, fabsf(kv[i][e]));
-            const float vq = ok ? ((fv[e] + 0.0f) - mv[e]) * iv[e] : 0.f;
-            vt[(ch * 8 + e) * KBLOCK + pos] = (uint8_t)e4m3_code(vq);
+        for (int i = 0; i < NI; i++) {
+            const int kl = slot + i * TPI;
+            const bool ok = blk * KBLOCK + kl < g.tk;
+            float fk[8], fv[8];
+            unpack8(kraw[i], fk, f16);
+            unpack8(vraw[i], fv, f16);
+            const int pos = v8_position(kl);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                // The reference sums the (one) member from 0.0f first: -0 becomes +0.
+                kv[i][e] = ok ? (fk[e] + 0.0f) - mk[e] : 0.f;
+                amax = fmaxf(amax, fabsf(kv[i][e]));
+                const float vq = ok ? ((fv[e] + 0.0f) - mv[e]) * iv[e] : 0.f;
+                vt[(ch * 8 + e) * KBLOCK + pos] = (uint8_t)e4m3_code(vq);
+            }
+        }
+    } else {
+        __syncthreads();
+        const int cells = g.merge * g.merge;  // uniform bound of the member loop
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int kl = slot + i * TPI;
+            const int j = blk * KBLOCK + kl;
+            const bool ok = j < g.tk;
+            int base = 0, nx = 1;
+            const int cnt = ok ? merged_members(g, j, base, nx) : 0;
+            float ks[8], vs[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) ks[e] = vs[e] = 0.f;
+            for (int m = 0; m < cells; m++) {
+                const bool mok = m < cnt;
+                const int tok = base + (mok ? (m / nx) * g.grid_w + m % nx : 0);
+                float fk[8], fv[8];
+                unpack8(load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, mok), fk, f16);
+                unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, mok), fv, f16);
+                if (mok) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        ks[e] += fk[e];
+                        vs[e] += fv[e];
+                    }
+                }
+            }
+            const float rc = cnt > 0 ? 1.0f / (float)cnt : 0.f;
+            const int pos = v8_position(kl);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                kv[i][e] = ok ? __builtin_fmaf(ks[e], rc, -mk[e]) : 0.f;
+                amax = fmaxf(amax, fabsf(kv[i][e]));
+                const float vq = ok ? __builtin_fmaf(vs[e], rc, -mv[e]) * iv[e] : 0.f;
+                vt[(ch * 8 + e) * KBLOCK + pos] = (uint8_t)e4m3_code(vq);
+            }
         }
     }
     amax = wave_max(amax);
@@ -284,6 +329,12 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
     uint8_t* vo = v8 + (bhk * g.kblocks + blk) * (long long)(D * KBLOCK);
     for (int c = tid; c < D * KBLOCK / 16; c += 256)
         reinterpret_cast<uint4*>(vo)[c] = reinterpret_cast<const uint4*>(vt)[c];
+    // The merge bias depends on the key alone (sage_quant.cu:321-325).
+    if (g.merge > 1 && b == 0 && hk == 0 && tid < KBLOCK) {
+        const int j = blk * KBLOCK + tid;
+        int base, nx;
+        kbias[j] = j < g.tk ? log2_count(merged_members(g, j, base, nx)) : __uint_as_float(0xff800000u);
+    }
 }
 
 template <int D>
@@ -297,7 +348,7 @@ static hipError_t launch_prologue_d(const uint16_t* q, const uint16_t* k, const 
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(sage_quant_kv<D>, dim3(g.kblocks, g.kv_heads, g.batch), dim3(256), 0, s, k, v, w.stats, w.k8,
-                       w.k_scale, w.v8, g);
+                       w.k_scale, w.v8, w.kbias, g);
     return hipGetLastError();
 }
 

@@ -24,7 +24,10 @@ def run(torch, p, q, k, v, out_dtype=None, q_layout="bthd", out_layout="bthd", w
 
     B, T, H, HK, D = p.batch, p.tokens, p.heads, p.hk, p.head_dim
     sa = S.SageAttention(None, D)
-    ws = sa.workspace(S.Shape(B, H, T, p.kv_heads))
+    merge = S.KvMerge.Dense
+    if p.merge > 1:
+        merge = S.KvMerge.Pool(p.merge, S.FrameLayout(*p.layout))
+    ws = sa.workspace(S.Shape(B, H, T, p.kv_heads), merge)
     od = p.dtype if out_dtype is None else out_dtype
     tdt = torch.bfloat16 if od == 0 else torch.float16
     if q_layout == "packed" and H == HK:
@@ -63,11 +66,14 @@ def run(torch, p, q, k, v, out_dtype=None, q_layout="bthd", out_layout="bthd", w
             "v8": v8_logical(get("v8"), B, HK, plan.tk_pad, D),
             "stats": get("stats").reshape(B, HK, 4, D),
         }
+        if p.merge > 1:
+            pro["kbias"] = get("kbias").reshape(plan.tk_pad)
     return pro, o
 
 
 def assert_prologue_equal(got: dict, want: dict) -> None:
-    for name in ("q8", "q_scale", "k8", "k_scale", "v8", "stats"):
+    names = ("q8", "q_scale", "k8", "k_scale", "v8", "stats") + (("kbias",) if "kbias" in got else ())
+    for name in names:
         a, b = got[name], want[name]
         assert a.shape == b.shape, (name, a.shape, b.shape)
         if a.dtype == np.float32:
