@@ -133,8 +133,11 @@ typedef struct sage_tensor_mut {
 
 /* Options (mod.rs:313-335). has_softmax_scale = 0 means the default
  * 1/sqrt(head_dim). qk_norm_params != NULL asks for the fused QK LayerNorm
- * (mod.rs:337-344), which returns SAGE_ERR_UNSUPPORTED in this build.
- * causal is an extension (keys j > i are masked). */
+ * (QkNorm, mod.rs:337-344): a device pointer to qk_norm_len >= 4 * head_dim
+ * floats, [q weight, q bias, k weight, k bias], applied to every Q and K head
+ * row before the statistics and quantisation read it (eps qk_norm_eps);
+ * fewer floats is SAGE_ERR_INVALID. causal is an extension (keys j > i are
+ * masked). */
 typedef struct sage_options {
     float softmax_scale;
     int32_t has_softmax_scale;

@@ -36,7 +36,7 @@ class _Problem(C.Structure):
         ("v_sb", C.c_longlong), ("v_st", C.c_longlong), ("v_sh", C.c_longlong),
         ("q_mul", C.c_float), ("smooth_k", C.c_int), ("smooth_v", C.c_int), ("v_range", C.c_float),
         ("merge", C.c_int), ("frames", C.c_int), ("special", C.c_int), ("grid_h", C.c_int), ("grid_w", C.c_int),
-        ("dense_frames", C.c_int),
+        ("dense_frames", C.c_int), ("ln", C.c_void_p), ("ln_eps", C.c_float),
     ]
 
 
@@ -93,6 +93,8 @@ def lib() -> C.CDLL:
         l.oracle_members.restype = C.c_int
         l.oracle_members.argtypes = [C.POINTER(_Problem), C.c_int, vp]
         l.oracle_log2_count.restype = C.c_float
+        l.oracle_layernorm.argtypes = [vp, vp, C.c_int, vp, vp, C.c_float]
+        l.oracle_layernorm_f64.argtypes = [vp, vp, C.c_int, vp, vp, C.c_float]
         l.oracle_log2_count.argtypes = [C.c_int]
         l.oracle_attention_f64.argtypes = [C.POINTER(_Problem), C.c_int, C.c_float, vp, vp, vp, vp, C.c_int, vp, C.c_int]
         l.oracle_sage_emulate.argtypes = [C.POINTER(_Problem), C.c_int, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int, vp,
@@ -173,6 +175,14 @@ class Problem:
     # KV merging (KvMerge::Pool): stride 1 = dense; layout = (frames, special, grid_h, grid_w, dense_frames)
     merge: int = 1
     layout: tuple = (1, 0, 0, 0, 0)
+    # QK LayerNorm (QkNorm): None, or [4 * head_dim] float32 (q weight, q bias, k weight, k bias)
+    ln: np.ndarray | None = field(default=None, compare=False)
+    ln_eps: float = 1e-5
+
+    def __post_init__(self):
+        if self.ln is not None:
+            self.ln = np.ascontiguousarray(self.ln, dtype=np.float32).reshape(-1)
+            assert self.ln.size >= 4 * self.head_dim
 
     @property
     def hk(self) -> int:
@@ -213,7 +223,8 @@ class Problem:
         k = self.strides.get("k", dflt(self.hk))
         v = self.strides.get("v", dflt(self.hk))
         return _Problem(self.batch, self.heads, self.hk, t, d, self.dtype, *q, *k, *v, float(self.q_mul()),
-                        int(self.smooth_k), int(self.smooth_v), 448.0, int(self.merge), *self.layout)
+                        int(self.smooth_k), int(self.smooth_v), 448.0, int(self.merge), *self.layout,
+                        None if self.ln is None else self.ln.ctypes.data, float(self.ln_eps))
 
 
 @dataclass
@@ -298,6 +309,22 @@ def sage_emulate(p: Problem, pro: dict, rows=None, out_dtype: int = BF16, thread
                               _p(pro["k_scale"]), _p(pro["v8"]), _p(pro["stats"]), _p(kb),
                               None if r is None else _p(r), R, _p(out), _p(o16), out_dtype, int(bool(fast_exp)), threads)
     return out, o16
+
+
+def layernorm(x: np.ndarray, ln_w: np.ndarray, ln_b: np.ndarray, eps: float = 1e-5, f64: bool = False) -> np.ndarray:
+    """Row-wise LayerNorm of x [..., D]: the prologue kernels' fp32 arithmetic
+    (sage_quant.cu:34-52, correctly rounded reciprocal square root), or with
+    f64=True the reference's CPU layer_norm (reference.rs:109-118)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(ln_w, dtype=np.float32)
+    b = np.ascontiguousarray(ln_b, dtype=np.float32)
+    D = x.shape[-1]
+    out = np.empty_like(x)
+    fn = lib().oracle_layernorm_f64 if f64 else lib().oracle_layernorm
+    xr, orow = x.reshape(-1, D), out.reshape(-1, D)
+    for i in range(xr.shape[0]):
+        fn(xr[i].ctypes.data, orow[i].ctypes.data, D, _p(w), _p(b), C.c_float(eps))
+    return out
 
 
 def log2_count(n: int) -> float:

@@ -230,6 +230,85 @@ void oracle_reference_synthetic(int batch, int tokens, int heads, int d, uint64_
 
 static size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
 
+/* ------------------------------------------------------------- LayerNorm */
+
+/* The xor butterfly of n lane values (s_c <- s_c + s_(c^o), o = 1, 2, ..,
+ * n/2); every lane ends with the same sum. */
+static void lane_butterfly(float* s, int n) {
+    float t[32];
+    for (int o = 1; o < n; o <<= 1) {
+        for (int c = 0; c < n; c++) t[c] = s[c] + s[c ^ o];
+        memcpy(s, t, sizeof(float) * (size_t)n);
+    }
+}
+
+/* sg_layernorm (sage_quant.cu:34-52) as the prologue kernels compute it. Lane
+ * c of the D/8 lanes that hold a row owns channels 8c..8c+7:
+ *   s_c = ((0 + x_8c) + x_8c+1) + ... + x_8c+7, the lane sums meeting in an
+ *   xor butterfly over distances 1, 2, .., D/16; mean = s * (1/D);
+ *   the squared deviations the same way, each step fmaf(x - mean, x - mean, s2);
+ *   rstd = 1 / sqrt(fmaf(s2, 1/D, eps)), the square root and the divide each
+ *   correctly rounded;
+ *   y = fmaf((x - mean) * rstd, w, b).
+ * The fused forms are NVRTC's default contraction of the reference's
+ * `s2 += d * d`, `s2 * (1.0f / D) + eps` and `(x - mean) * rstd * w + b`.
+ * The reference takes rsqrtf, an approximation whose rounding it does not
+ * state; this build takes the correctly rounded form instead, so a normalised
+ * value can differ from the reference GPU's in its last bits.
+ * Pinned: against the reference's f64 layer_norm (reference.rs:109-118) on
+ * random, offset, eps-dominated and constant rows, and through check_prologue
+ * with QK LayerNorm (tests.rs:448-466, 476-594), in tests. */
+void oracle_layernorm(const float* x, float* y, int D, const float* w, const float* b, float eps) {
+    const int CH = D / 8;
+    float ls[32], l2[32];
+    for (int c = 0; c < CH; c++) {
+        float s = 0.f;
+        for (int e = 0; e < 8; e++) s += x[8 * c + e];
+        ls[c] = s;
+    }
+    lane_butterfly(ls, CH);
+    const float mean = ls[0] * (1.0f / (float)D);
+    for (int c = 0; c < CH; c++) {
+        float s2 = 0.f;
+        for (int e = 0; e < 8; e++) {
+            const float d = x[8 * c + e] - mean;
+            s2 = fmaf(d, d, s2);
+        }
+        l2[c] = s2;
+    }
+    lane_butterfly(l2, CH);
+    const float rstd = 1.0f / sqrtf(fmaf(l2[0], 1.0f / (float)D, eps));
+    for (int i = 0; i < D; i++) y[i] = fmaf((x[i] - mean) * rstd, w[i], b[i]);
+}
+
+/* reference.rs:109-118 (layer_norm): the f64 LayerNorm of the reference's
+ * tests. Pinned: numpy float64 and closed forms in tests. */
+void oracle_layernorm_f64(const float* x, float* y, int D, const float* w, const float* b, float eps) {
+    double mean = 0.0, var = 0.0;
+    for (int i = 0; i < D; i++) mean += (double)x[i];
+    mean /= (double)D;
+    for (int i = 0; i < D; i++) var += ((double)x[i] - mean) * ((double)x[i] - mean);
+    var /= (double)D;
+    const double rstd = 1.0 / sqrt(var + (double)eps);
+    for (int i = 0; i < D; i++) y[i] = (float)(((double)x[i] - mean) * rstd * (double)w[i] + (double)b[i]);
+}
+
+/* Head row `tok` of a 16-bit [b][t][h][d] input, decoded. */
+static void read_row(const oracle_problem* p, const uint16_t* x, long long sb, long long st, long long sh, int b,
+                     int h, int tok, float* out) {
+    const uint16_t* r = x + b * sb + (long long)tok * st + h * sh;
+    for (int d = 0; d < p->head_dim; d++) out[d] = dec16(r[d], p->dtype);
+}
+
+/* Q (is_k = 0) or K (is_k = 1) head row, decoded and, under QK LayerNorm,
+ * normalised as the prologue kernels do (sage_quant.cu:89-90, :271). */
+static void qk_row(const oracle_problem* p, const uint16_t* x, int is_k, int b, int h, int tok, float* out) {
+    const int D = p->head_dim;
+    if (is_k) read_row(p, x, p->k_sb, p->k_st, p->k_sh, b, h, tok, out);
+    else read_row(p, x, p->q_sb, p->q_st, p->q_sh, b, h, tok, out);
+    if (p->ln) oracle_layernorm(out, out, D, p->ln + (is_k ? 2 : 0) * D, p->ln + (is_k ? 3 : 1) * D, p->ln_eps);
+}
+
 /* Per (b, kv head) channel statistics in the reference's fp32 order
  * (sage_quant.cu:73-80,97-107,129-159 then :163-205):
  *   slot s of a 128-token tile sums its tokens t*128 + s + TPI*i in i order
@@ -246,25 +325,29 @@ static void kv_stats(const oracle_problem* p, int b, int hk, const uint16_t* k, 
     const int q_tiles = (int)(round_up((size_t)N, ORACLE_QTILE) / ORACLE_QTILE);
     float* part = (float*)malloc(sizeof(float) * (size_t)q_tiles * 4 * D);
     float* P = (float*)malloc(sizeof(float) * (size_t)TPI * 4 * D); /* slot partials [s][stat][d] */
+    float fk[256], fv[256];
     for (int t = 0; t < q_tiles; t++) {
-        for (int s = 0; s < TPI; s++)
+        for (int s = 0; s < TPI; s++) {
+            float* Ps = P + (size_t)s * 4 * D;
             for (int d = 0; d < D; d++) {
-                float ks = 0.f, vs = 0.f, vmn = 3.0e38f, vmx = -3.0e38f;
-                for (int i = 0; i < NI; i++) {
-                    int tok = t * ORACLE_QTILE + s + TPI * i;
-                    if (tok >= N) continue;
-                    float fk = dec16(k[b * p->k_sb + (long long)tok * p->k_st + hk * p->k_sh + d], p->dtype);
-                    float fv = dec16(v[b * p->v_sb + (long long)tok * p->v_st + hk * p->v_sh + d], p->dtype);
-                    ks += fk;
-                    vs += fv;
-                    vmn = fminf(vmn, fv);
-                    vmx = fmaxf(vmx, fv);
-                }
-                P[((size_t)s * 4 + 0) * D + d] = ks;
-                P[((size_t)s * 4 + 1) * D + d] = vs;
-                P[((size_t)s * 4 + 2) * D + d] = vmn;
-                P[((size_t)s * 4 + 3) * D + d] = vmx;
+                Ps[d] = 0.f;
+                Ps[D + d] = 0.f;
+                Ps[2 * D + d] = 3.0e38f;
+                Ps[3 * D + d] = -3.0e38f;
             }
+            for (int i = 0; i < NI; i++) {
+                int tok = t * ORACLE_QTILE + s + TPI * i;
+                if (tok >= N) continue;
+                qk_row(p, k, 1, b, hk, tok, fk);
+                read_row(p, v, p->v_sb, p->v_st, p->v_sh, b, hk, tok, fv);
+                for (int d = 0; d < D; d++) {
+                    Ps[d] += fk[d];
+                    Ps[D + d] += fv[d];
+                    Ps[2 * D + d] = fminf(Ps[2 * D + d], fv[d]);
+                    Ps[3 * D + d] = fmaxf(Ps[3 * D + d], fv[d]);
+                }
+            }
+        }
         const int spw = 32 / CH; /* slots per 32-lane warp: 2 (D=128) or 4 (D=64) */
         for (int stat = 0; stat < 4; stat++)
             for (int d = 0; d < D; d++) {
@@ -328,21 +411,19 @@ static void kv_stats(const oracle_problem* p, int b, int hk, const uint16_t* k, 
 static void quant_q(const oracle_problem* p, int b, int h, const uint16_t* q, int8_t* q8, float* qsc) {
     const int D = p->head_dim, N = p->tokens;
     const size_t tq_pad = round_up((size_t)N, ORACLE_QTILE);
+    float x[ORACLE_QGROUP][256];
     for (size_t g = 0; g < tq_pad / ORACLE_QGROUP; g++) {
         float amax = 0.f;
         for (int r = 0; r < ORACLE_QGROUP; r++) {
             int tok = (int)(g * ORACLE_QGROUP) + r;
-            if (tok >= N) continue;
-            for (int d = 0; d < D; d++)
-                amax = fmaxf(amax, fabsf(dec16(q[b * p->q_sb + (long long)tok * p->q_st + h * p->q_sh + d], p->dtype)));
+            if (tok < N) qk_row(p, q, 0, b, h, tok, x[r]);
+            else memset(x[r], 0, sizeof(float) * (size_t)D);
+            for (int d = 0; d < D; d++) amax = fmaxf(amax, fabsf(x[r][d]));
         }
         const float inv = amax > 0.f ? 127.0f / amax : 0.f;
         for (int r = 0; r < ORACLE_QGROUP; r++) {
             int tok = (int)(g * ORACLE_QGROUP) + r;
-            for (int d = 0; d < D; d++) {
-                float x = tok < N ? dec16(q[b * p->q_sb + (long long)tok * p->q_st + h * p->q_sh + d], p->dtype) : 0.f;
-                q8[(size_t)tok * D + d] = (int8_t)oracle_s8(x * inv);
-            }
+            for (int d = 0; d < D; d++) q8[(size_t)tok * D + d] = (int8_t)oracle_s8(x[r][d] * inv);
         }
         qsc[g] = amax * (1.0f / 127.0f) * p->q_mul;
     }
@@ -421,6 +502,7 @@ static void quant_kv(const oracle_problem* p, int b, int hk, const uint16_t* k, 
     const int D = p->head_dim, TK = oracle_merged_keys(p);
     const size_t tk_pad = round_up((size_t)TK, ORACLE_KBLOCK);
     float* kv = (float*)malloc(sizeof(float) * ORACLE_KBLOCK * D);
+    float ks[256], vs[256], fk[256], fv[256];
     int mem[16];
     for (size_t blk = 0; blk < tk_pad / ORACLE_KBLOCK; blk++) {
         float amax = 0.f;
@@ -428,16 +510,20 @@ static void quant_kv(const oracle_problem* p, int b, int hk, const uint16_t* k, 
             int j = (int)(blk * ORACLE_KBLOCK) + r;
             const int n = j < TK ? oracle_members(p, j, mem) : 0;
             const float rc = n > 0 ? 1.0f / (float)n : 0.f;
+            for (int d = 0; d < D; d++) ks[d] = vs[d] = 0.f;
+            for (int m = 0; m < n; m++) {
+                qk_row(p, k, 1, b, hk, mem[m], fk);
+                read_row(p, v, p->v_sb, p->v_st, p->v_sh, b, hk, mem[m], fv);
+                for (int d = 0; d < D; d++) {
+                    ks[d] += fk[d];
+                    vs[d] += fv[d];
+                }
+            }
             for (int d = 0; d < D; d++) {
                 float x = 0.f, vq = 0.f;
                 if (n > 0) {
-                    float ks = 0.f, vs = 0.f;
-                    for (int m = 0; m < n; m++) {
-                        ks += dec16(k[b * p->k_sb + (long long)mem[m] * p->k_st + hk * p->k_sh + d], p->dtype);
-                        vs += dec16(v[b * p->v_sb + (long long)mem[m] * p->v_st + hk * p->v_sh + d], p->dtype);
-                    }
-                    x = fmaf(ks, rc, -st[d]);
-                    vq = fmaf(vs, rc, -st[D + d]) * st[3 * D + d];
+                    x = fmaf(ks[d], rc, -st[d]);
+                    vq = fmaf(vs[d], rc, -st[D + d]) * st[3 * D + d];
                 }
                 kv[r * D + d] = x;
                 amax = fmaxf(amax, fabsf(x));
@@ -489,7 +575,8 @@ int oracle_prologue(const oracle_problem* p, const uint16_t* q, const uint16_t* 
  * inputs; causal rows see keys j <= i; Q head h reads KV head h / (H/HKV).
  * KV merging pools K and V per (b, kv head) first, as reference.rs:113-143
  * does (f32 sums in member order, then / n in f32), and adds
- * log2(n_j) * ln 2 to key j's logits.
+ * log2(n_j) * ln 2 to key j's logits. Under QK LayerNorm the Q and K rows
+ * are normalised first by the reference's f64 layer_norm (tests.rs:448-466).
  * Pinned: closed forms in tests (uniform keys give the mean of V; one-hot
  * logits select one V row; V = const gives const), numpy/torch float64, and
  * the reference's merged == dense identity on uniform cells (tests.rs:193-232). */
@@ -503,21 +590,29 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
     float* vf = (float*)malloc(sizeof(float) * (size_t)B * HK * TK * D);
     double* kb = (double*)malloc(sizeof(double) * (size_t)TK);
     int mem[16];
+    float rk[256], rv[256];
     for (int j = 0; j < TK; j++) {
         const int n = oracle_members(p, j, mem);
         kb[j] = merging(p) ? (double)oracle_log2_count(n) * 0.69314718055994530942 : 0.0;
         for (int b = 0; b < B; b++)
-            for (int hk = 0; hk < HK; hk++)
-                for (int d = 0; d < D; d++) {
-                    float ks = 0.f, vs = 0.f;
-                    for (int m = 0; m < n; m++) {
-                        ks += dec16(k[b * p->k_sb + (long long)mem[m] * p->k_st + hk * p->k_sh + d], p->dtype);
-                        vs += dec16(v[b * p->v_sb + (long long)mem[m] * p->v_st + hk * p->v_sh + d], p->dtype);
+            for (int hk = 0; hk < HK; hk++) {
+                float* ko = kf + (((size_t)b * HK + hk) * TK + j) * D;
+                float* vo = vf + (((size_t)b * HK + hk) * TK + j) * D;
+                for (int d = 0; d < D; d++) ko[d] = vo[d] = 0.f;
+                for (int m = 0; m < n; m++) {
+                    read_row(p, k, p->k_sb, p->k_st, p->k_sh, b, hk, mem[m], rk);
+                    read_row(p, v, p->v_sb, p->v_st, p->v_sh, b, hk, mem[m], rv);
+                    if (p->ln) oracle_layernorm_f64(rk, rk, D, p->ln + 2 * D, p->ln + 3 * D, p->ln_eps);
+                    for (int d = 0; d < D; d++) {
+                        ko[d] += rk[d];
+                        vo[d] += rv[d];
                     }
-                    const size_t o = (((size_t)b * HK + hk) * TK + j) * D + d;
-                    kf[o] = n > 1 ? ks / (float)n : ks;
-                    vf[o] = n > 1 ? vs / (float)n : vs;
                 }
+                for (int d = 0; d < D; d++) {
+                    ko[d] /= (float)n;
+                    vo[d] /= (float)n;
+                }
+            }
     }
     set_threads(threads);
 #pragma omp parallel
@@ -525,12 +620,15 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
         double* logit = (double*)malloc(sizeof(double) * TK);
         double* acc = (double*)malloc(sizeof(double) * D);
         double* qi = (double*)malloc(sizeof(double) * D);
+        float qf[256];
 #pragma omp for schedule(dynamic) collapse(2)
         for (int bh = 0; bh < B * H; bh++)
             for (int ri = 0; ri < R; ri++) {
                 int b = bh / H, h = bh % H, hk = h / G;
                 int i = rows ? rows[ri] : ri;
-                for (int d = 0; d < D; d++) qi[d] = dec16(q[b * p->q_sb + (long long)i * p->q_st + h * p->q_sh + d], p->dtype);
+                read_row(p, q, p->q_sb, p->q_st, p->q_sh, b, h, i, qf);
+                if (p->ln) oracle_layernorm_f64(qf, qf, D, p->ln, p->ln + D, p->ln_eps);
+                for (int d = 0; d < D; d++) qi[d] = qf[d];
                 const float* kr0 = kf + ((size_t)b * HK + hk) * TK * D;
                 const float* vr0 = vf + ((size_t)b * HK + hk) * TK * D;
                 int nk = causal ? i + 1 : TK;

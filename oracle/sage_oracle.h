@@ -9,7 +9,8 @@
  *   - codecs            src/sage/reference.rs:8-70, cuda/sage_common.cu:76-99
  *   - splitmix64 RNG    src/sage/reference.rs:228-254
  *   - prologue          cuda/sage_quant.cu:59-206 (sg_prep, sg_finalize) and
- *                       :238-326 (sg_quant_kv), fp32 operation order kept
+ *                       :238-326 (sg_quant_kv), fp32 operation order kept;
+ *                       QK LayerNorm :34-52, KV merging :210-235
  *   - f64 attention     src/sage/reference.rs:148-184 (+ causal, GQA)
  *   - sage emulator     cuda/sage_attn.cu:262-344,402-421 semantics
  *   - error metrics     src/sage/reference.rs:202-225
@@ -54,7 +55,20 @@ typedef struct {
      * first `dense_frames` frames. */
     int merge;
     int frames, special, grid_h, grid_w, dense_frames;
+    /* QK LayerNorm (mod.rs:337-344, QkNorm): NULL is off, else [4][D] floats
+     * (q weight, q bias, k weight, k bias) applied to every Q and K head row
+     * before anything else reads it; V is never normalised. */
+    const float* ln;
+    float ln_eps;
 } oracle_problem;
+
+/* LayerNorm of one D-channel row in the prologue kernels' fp32 arithmetic
+ * (restates sage_quant.cu:34-52 with the reciprocal square root correctly
+ * rounded; see sage_oracle.c). x and y may alias. */
+void oracle_layernorm(const float* x, float* y, int D, const float* w, const float* b, float eps);
+/* The reference's own CPU LayerNorm (reference.rs:109-118): f64 mean, biased
+ * variance and 1/sqrt, rounded to f32 at the end. x and y may alias. */
+void oracle_layernorm_f64(const float* x, float* y, int D, const float* w, const float* b, float eps);
 
 /* Keys after merging (FrameLayout::merged_keys, mod.rs:293-299); tokens when dense. */
 int oracle_merged_keys(const oracle_problem* p);

@@ -379,17 +379,15 @@ sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage
     if (q->dtype != k->dtype || q->dtype != v->dtype)
         return fail(SAGE_ERR_INVALID, "Q, K and V must share one element type");
     if (q->dtype != SAGE_BF16 && q->dtype != SAGE_F16) return fail(SAGE_ERR_INVALID, "unknown dtype %d", q->dtype);
-    if (opts->qk_norm_params) {
-        if (opts->qk_norm_len < 4 * d)
-            return fail(SAGE_ERR_INVALID, "QK-norm params hold %llu floats, need %llu", (u64)opts->qk_norm_len,
-                        (u64)(4 * d));
-        return fail(SAGE_ERR_UNSUPPORTED, "the fused QK LayerNorm (QkNorm) is not supported by this build");
-    }
+    if (opts->qk_norm_params && opts->qk_norm_len < 4 * d)
+        return fail(SAGE_ERR_INVALID, "QK-norm params hold %llu floats, need %llu", (u64)opts->qk_norm_len,
+                    (u64)(4 * d));
     // Causal masking (an extension) is defined over token positions; merged
     // keys have none.
     if (opts->causal && plan.merge.stride != 1)
         return fail(SAGE_ERR_UNSUPPORTED, "causal masking over merged keys (KvMerge::Pool) is not supported");
     int flags = 0;
+    if (opts->qk_norm_params) flags |= sage::F_LN_Q | sage::F_LN_K;  // mod.rs:715-717
     if (opts->smooth_k) flags |= sage::F_SMOOTH_K;
     if (opts->smooth_v) flags |= sage::F_SMOOTH_V;
     if (opts->causal) flags |= sage::F_CAUSAL;
@@ -420,6 +418,7 @@ sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage
     g.flags = flags;
     g.q_mul = scale * log2e;
     g.v_range = SAGE_FP8_MAX;
+    g.ln_eps = opts->qk_norm_params ? opts->qk_norm_eps : 1e-5f;
     // Merge geometry (mod.rs:727-770): a dense plan is one frame of `tokens`
     // tokens with merge = 1.
     const sage_frame_layout& l = plan.merge.layout;
@@ -438,7 +437,7 @@ sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage
     sage::PrologueBufs bufs{ws->q8, ws->q_scale, ws->k8, ws->k_scale, ws->v8, ws->stats, ws->part, ws->kbias};
     hipError_t e = sage::launch_prologue((int)d, static_cast<const uint16_t*>(q->data),
                                          static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
-                                         bufs, g, s->stream);
+                                         opts->qk_norm_params, bufs, g, s->stream);
     if (e != hipSuccess) return hip_fail(e, "launch sage prologue");
     ws->geom = g;
     ws->prepared = true;

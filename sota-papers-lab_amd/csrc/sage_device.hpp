@@ -14,7 +14,9 @@ constexpr int QTILE = 128;  // queries per prologue tile (one K/V statistics par
 constexpr int KBLOCK = 64;  // keys per K scale and per V block
 
 enum : int {
-    F_SMOOTH_K = 4,  // flag values of the reference's SgGeom::flags (sage_common.cu:26-29)
+    F_LN_Q = 1,      // flag values of the reference's SgGeom::flags (sage_common.cu:26-29)
+    F_LN_K = 2,
+    F_SMOOTH_K = 4,
     F_SMOOTH_V = 8,
     F_CAUSAL = 16,   // extensions
     F_IN_F16 = 32,
@@ -40,6 +42,7 @@ struct Geom {
     // grid in merge x merge cells (merged_w cells a row, merged_frame keys a
     // frame), keeping the `special` tokens and the first dense_frames frames.
     int merge, frame_tokens, special, grid_h, grid_w, merged_frame, merged_w, dense_frames;
+    float ln_eps;  // QK LayerNorm epsilon (F_LN_Q / F_LN_K)
 };
 
 // Members of merged key j (sage_quant.cu:210-235): returns the count; member

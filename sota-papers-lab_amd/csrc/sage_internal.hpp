@@ -32,7 +32,9 @@ struct AttendBufs {
     void* out;
 };
 
-hipError_t launch_prologue(int head_dim, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+// ln: [4][head_dim] QK LayerNorm parameters (q weight, q bias, k weight,
+// k bias), read only under F_LN_Q / F_LN_K; may be null otherwise.
+hipError_t launch_prologue(int head_dim, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ln,
                            const PrologueBufs& w, const Geom& g, hipStream_t s);
 
 // Rows of queries one attention workgroup owns.

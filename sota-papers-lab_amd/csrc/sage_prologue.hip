@@ -5,6 +5,7 @@
 //   sage_prep      grid (q_tiles, kv_heads, batch): per 128-token tile, the
 //                  partial K sum, V sum, V min, V max of every channel, and
 //                  INT8 Q of the `group` query heads that share the KV head
+//                  (Q and K rows LayerNormed first under QK LayerNorm)
 //   sage_finalize  grid (kv_heads, batch): K mean, V mean, V scale, 1/V scale
 //   sage_quant_kv  grid (kblocks, kv_heads, batch): smoothed INT8 K and FP8 V,
 //                  V transposed per 64-key block into the MFMA operand order;
@@ -33,11 +34,47 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
-// sage_quant.cu:59-160 (sg_prep), without LayerNorm.
+// LayerNorm of one head row (sage_quant.cu:34-52) whose D channels lie on
+// D/8 consecutive lanes, 8 a lane (ch = lane's chunk); every lane of the wave
+// calls it. The lane sums meet in the reference's xor butterfly over
+// distances 1 .. D/16; the square deviations accumulate fused (fmaf), the
+// variance takes fmaf(s2, 1/D, eps) and the output fmaf((x - mean) * rstd,
+// w, b) -- the reference's expressions under NVRTC's default contraction.
+// rstd is 1 / sqrt(.) with the square root and the divide each correctly
+// rounded (the reference's rsqrtf is an approximation whose rounding it does
+// not state), so the kernel and the CPU oracle agree bit for bit.
 template <int D>
+__device__ __forceinline__ void layernorm8(float* x, const float* __restrict__ w, const float* __restrict__ bias,
+                                           int ch, float eps) {
+    constexpr int CH = D / 8;
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) s += x[e];
+#pragma unroll
+    for (int o = 1; o < CH; o <<= 1) s += __shfl_xor(s, o, 64);
+    const float mean = s * (1.0f / D);
+    float s2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float d = x[e] - mean;
+        s2 = __builtin_fmaf(d, d, s2);
+    }
+#pragma unroll
+    for (int o = 1; o < CH; o <<= 1) s2 += __shfl_xor(s2, o, 64);
+    const float rstd = 1.0f / sqrtf(__builtin_fmaf(s2, 1.0f / D, eps));
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = __builtin_fmaf((x[e] - mean) * rstd, w[ch * 8 + e], bias[ch * 8 + e]);
+}
+
+// sage_quant.cu:59-160 (sg_prep). Under QK LayerNorm (LN, the F_LN_Q and
+// F_LN_K flags together as the reference sets them) every K row is normalised
+// before the statistics read it and every Q row before its amax; the LN-free
+// instantiation keeps the dense kernel's registers.
+template <int D, bool LN>
 __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                                                 const uint16_t* __restrict__ v, int8_t* __restrict__ q8,
-                                                 float* __restrict__ q_scale, float* __restrict__ part, Geom g) {
+                                                 const uint16_t* __restrict__ v, const float* __restrict__ ln,
+                                                 int8_t* __restrict__ q8, float* __restrict__ q_scale,
+                                                 float* __restrict__ part, Geom g) {
     constexpr int CH = D / 8;        // 16-byte chunks per head row
     constexpr int TPI = 256 / CH;    // tokens per iteration
     constexpr int NI = QTILE / TPI;  // iterations
@@ -69,10 +106,11 @@ __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q,
 #pragma unroll
     for (int i = 0; i < NI; i++) {
         const int tok = tile * QTILE + slot + i * TPI;
+        float fk[8], fv[8];
+        unpack8(kraw[i], fk, f16);
+        unpack8(vraw[i], fv, f16);
+        if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
         if (tok < g.tokens) {
-            float fk[8], fv[8];
-            unpack8(kraw[i], fk, f16);
-            unpack8(vraw[i], fv, f16);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 ks[e] += fk[e];
@@ -131,6 +169,13 @@ __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q,
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             unpack8(qraw[i], qv[i], f16);
+            if (LN) {
+                layernorm8<D>(qv[i], ln, ln + D, ch, g.ln_eps);
+                if (tile * QTILE + slot + i * TPI >= g.tokens) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) qv[i][e] = 0.f;  // padding rows stay zero
+                }
+            }
             float amax = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(qv[i][e]));
@@ -218,8 +263,11 @@ __global__ __launch_bounds__(4 * D) void sage_finalize(const float* __restrict__
 // A merged key sums its members in order from 0.0f and takes
 // fmaf(sum, 1/n, -mean): NVRTC's default contraction of the reference's
 // `sum * rc - mean`, equal to the dense (k + 0) - mean when n = 1.
-template <int D>
+// Under QK LayerNorm (LN) each K row (each member, when merging) is
+// normalised before it is summed (sage_quant.cu:271).
+template <int D, bool LN>
 __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                                     const float* __restrict__ ln,
                                                      const float* __restrict__ stats, int8_t* __restrict__ k8,
                                                      float* __restrict__ k_scale, uint8_t* __restrict__ v8,
                                                      float* __restrict__ kbias, Geom g) {
@@ -262,6 +310,7 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
             float fk[8], fv[8];
             unpack8(kraw[i], fk, f16);
             unpack8(vraw[i], fv, f16);
+            if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
             const int pos = v8_position(kl);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
@@ -291,6 +340,7 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
                 float fk[8], fv[8];
                 unpack8(load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, mok), fk, f16);
                 unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, mok), fv, f16);
+                if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
                 if (mok) {
 #pragma unroll
                     for (int e = 0; e < 8; e++) {
@@ -337,24 +387,27 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
     }
 }
 
-template <int D>
-static hipError_t launch_prologue_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, const PrologueBufs& w,
-                                    const Geom& g, hipStream_t s) {
-    hipLaunchKernelGGL(sage_prep<D>, dim3(g.q_tiles, g.kv_heads, g.batch), dim3(256), 0, s, q, k, v, w.q8,
+template <int D, bool LN>
+static hipError_t launch_prologue_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ln,
+                                    const PrologueBufs& w, const Geom& g, hipStream_t s) {
+    hipLaunchKernelGGL((sage_prep<D, LN>), dim3(g.q_tiles, g.kv_heads, g.batch), dim3(256), 0, s, q, k, v, ln, w.q8,
                        w.q_scale, w.part, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(sage_finalize<D>, dim3(g.kv_heads, g.batch), dim3(4 * D), 0, s, w.part, w.stats, g);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(sage_quant_kv<D>, dim3(g.kblocks, g.kv_heads, g.batch), dim3(256), 0, s, k, v, w.stats, w.k8,
-                       w.k_scale, w.v8, w.kbias, g);
+    hipLaunchKernelGGL((sage_quant_kv<D, LN>), dim3(g.kblocks, g.kv_heads, g.batch), dim3(256), 0, s, k, v, ln, w.stats,
+                       w.k8, w.k_scale, w.v8, w.kbias, g);
     return hipGetLastError();
 }
 
-hipError_t launch_prologue(int head_dim, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+hipError_t launch_prologue(int head_dim, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ln,
                            const PrologueBufs& w, const Geom& g, hipStream_t s) {
-    return head_dim == 64 ? launch_prologue_d<64>(q, k, v, w, g, s) : launch_prologue_d<128>(q, k, v, w, g, s);
+    const bool norm = (g.flags & (F_LN_Q | F_LN_K)) == (F_LN_Q | F_LN_K);
+    if (head_dim == 64)
+        return norm ? launch_prologue_d<64, true>(q, k, v, ln, w, g, s) : launch_prologue_d<64, false>(q, k, v, ln, w, g, s);
+    return norm ? launch_prologue_d<128, true>(q, k, v, ln, w, g, s) : launch_prologue_d<128, false>(q, k, v, ln, w, g, s);
 }
 
 }  // namespace sage

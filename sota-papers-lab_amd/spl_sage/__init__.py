@@ -190,10 +190,20 @@ KvMerge.Dense = KvMerge(1, None)
 
 @dataclass
 class QkNorm:
-    """mod.rs:337-344 (accepted for validation; fusion is not in this build)."""
+    """mod.rs:337-344: the per-head LayerNorm of Q and K fused into the
+    prologue. `params` is a contiguous float32 device tensor holding
+    [q weight, q bias, k weight, k bias], head_dim floats each."""
 
     params: object  # torch tensor of 4 * head_dim floats
     eps: float = 1e-5
+
+    def _ptr(self) -> int:
+        import torch
+
+        p = self.params
+        if p.dtype != torch.float32 or not p.is_contiguous():
+            raise SageError(1, f"QK-norm params must be contiguous float32, got {p.dtype}")
+        return p.data_ptr()
 
 
 @dataclass
@@ -214,7 +224,7 @@ class Options:
         o.smooth_v = int(self.smooth_v)
         if self.qk_norm is not None:
             p = self.qk_norm.params
-            o.qk_norm_params = p.data_ptr()
+            o.qk_norm_params = self.qk_norm._ptr()
             o.qk_norm_len = p.numel()
             o.qk_norm_eps = self.qk_norm.eps
         o.causal = int(self.causal)

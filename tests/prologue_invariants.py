@@ -5,7 +5,9 @@ and every Q code within half a step; K mean within 1e-3 of the f64 mean; K
 scale within 1e-4 of amax/127 and every K code within half a step; V
 de-quantised within |v - mean|/16 + scale * 2^-8. With KV merging the keys are
 the reference's pooled K and V (reference.rs:113-143: f32 sums in member order,
-then / n) and every kbias entry is log2(n) within 1e-6, -inf past the keys."""
+then / n) and every kbias entry is log2(n) within 1e-6, -inf past the keys.
+Under QK LayerNorm the Q and K rows are first normalised by the reference's f64
+layer_norm (reference.rs:109-118), as tests.rs:448-466 (reference_head) does."""
 from __future__ import annotations
 
 import numpy as np
@@ -28,9 +30,23 @@ def pool_kv(p, kk: np.ndarray, vv: np.ndarray):
     return km, vm, n
 
 
+def layer_norm_rows(x: np.ndarray, w: np.ndarray, b: np.ndarray, eps: float) -> np.ndarray:
+    """reference.rs:109-118 over the last axis: f64 mean and biased variance,
+    1 / sqrt(var + eps), the affine map in f64, rounded to f32."""
+    x64 = x.astype(np.float64)
+    mean = x64.mean(axis=-1, keepdims=True)
+    var = ((x64 - mean) ** 2).mean(axis=-1, keepdims=True)
+    rstd = 1.0 / np.sqrt(var + np.float64(np.float32(eps)))
+    return ((x64 - mean) * rstd * w.astype(np.float64) + b.astype(np.float64)).astype(np.float32)
+
+
 def check_prologue(p, qf: np.ndarray, kf: np.ndarray, vf: np.ndarray, pro: dict, smooth: bool = True) -> None:
     """qf, kf, vf: decoded inputs [B,T,H,D] / [B,T,HKV,D] float32."""
     B, T, H, HK, D = p.batch, p.tokens, p.heads, p.hk, p.head_dim
+    if p.ln is not None:
+        ln = p.ln.reshape(-1)[: 4 * D].reshape(4, D)
+        qf = layer_norm_rows(qf, ln[0], ln[1], p.ln_eps)
+        kf = layer_norm_rows(kf, ln[2], ln[3], p.ln_eps)
     TK = p.tk
     qmul = np.float32(np.float32(1.4426950408889634) / np.sqrt(np.float32(D))) if p.softmax_scale is None \
         else np.float32(np.float32(p.softmax_scale) * np.float32(1.4426950408889634))

@@ -48,7 +48,11 @@ def run(torch, p, q, k, v, out_dtype=None, q_layout="bthd", out_layout="bthd", w
     else:
         out = torch.empty((B, T, H, D), dtype=tdt, device="cuda")
         om = S.TensorMut(out)
-    opts = S.Options(softmax_scale=p.softmax_scale, smooth_k=p.smooth_k, smooth_v=p.smooth_v, causal=p.causal)
+    qk_norm = None
+    if p.ln is not None:
+        qk_norm = S.QkNorm(torch.from_numpy(p.ln.copy()).to("cuda"), float(p.ln_eps))
+    opts = S.Options(softmax_scale=p.softmax_scale, smooth_k=p.smooth_k, smooth_v=p.smooth_v, causal=p.causal,
+                     qk_norm=qk_norm)
     sa.forward(ws, qt, kt, vt, om, opts)
     torch.cuda.synchronize()
     o = from_device16(out)
