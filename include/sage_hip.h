@@ -52,8 +52,10 @@ typedef enum sage_status {
  * (sage_common.cu:66-80); fp16 is an extension. */
 typedef enum sage_dtype { SAGE_BF16 = 0, SAGE_F16 = 1 } sage_dtype;
 
-/* PvAccum (mod.rs:170-181). Only F32 is implemented; F16 returns
- * SAGE_ERR_UNSUPPORTED. */
+/* PvAccum (mod.rs:170-185). F16 quantises V to +-SAGE_PV16_V_RANGE, as the
+ * reference's F16 mode does, so the prologue's codes and scales are that
+ * mode's. gfx950's FP8 MFMA accumulates in fp32 only: the P.V block partials
+ * stay fp32 under both settings (at least as accurate as f16 partials). */
 typedef enum sage_pv_accum { SAGE_PV_F32 = 0, SAGE_PV_F16 = 1 } sage_pv_accum;
 
 /* Tile (mod.rs:116-168), re-read for CDNA4: `warps` = wave64s per workgroup,

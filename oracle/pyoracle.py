@@ -36,7 +36,7 @@ class _Problem(C.Structure):
         ("v_sb", C.c_longlong), ("v_st", C.c_longlong), ("v_sh", C.c_longlong),
         ("q_mul", C.c_float), ("smooth_k", C.c_int), ("smooth_v", C.c_int), ("v_range", C.c_float),
         ("merge", C.c_int), ("frames", C.c_int), ("special", C.c_int), ("grid_h", C.c_int), ("grid_w", C.c_int),
-        ("dense_frames", C.c_int), ("ln", C.c_void_p), ("ln_eps", C.c_float),
+        ("dense_frames", C.c_int), ("ln", C.c_void_p), ("ln_eps", C.c_float), ("pv16", C.c_int),
     ]
 
 
@@ -93,6 +93,8 @@ def lib() -> C.CDLL:
         l.oracle_members.restype = C.c_int
         l.oracle_members.argtypes = [C.POINTER(_Problem), C.c_int, vp]
         l.oracle_log2_count.restype = C.c_float
+        l.oracle_round_f16.restype = C.c_double
+        l.oracle_round_f16.argtypes = [C.c_double]
         l.oracle_layernorm.argtypes = [vp, vp, C.c_int, vp, vp, C.c_float]
         l.oracle_layernorm_f64.argtypes = [vp, vp, C.c_int, vp, vp, C.c_float]
         l.oracle_log2_count.argtypes = [C.c_int]
@@ -178,6 +180,8 @@ class Problem:
     # QK LayerNorm (QkNorm): None, or [4 * head_dim] float32 (q weight, q bias, k weight, k bias)
     ln: np.ndarray | None = field(default=None, compare=False)
     ln_eps: float = 1e-5
+    # PvAccum::F16: V scaled to +-2.25 (PV16_V_RANGE) and f16 block partials in the emulator
+    pv16: bool = False
 
     def __post_init__(self):
         if self.ln is not None:
@@ -223,8 +227,9 @@ class Problem:
         k = self.strides.get("k", dflt(self.hk))
         v = self.strides.get("v", dflt(self.hk))
         return _Problem(self.batch, self.heads, self.hk, t, d, self.dtype, *q, *k, *v, float(self.q_mul()),
-                        int(self.smooth_k), int(self.smooth_v), 448.0, int(self.merge), *self.layout,
-                        None if self.ln is None else self.ln.ctypes.data, float(self.ln_eps))
+                        int(self.smooth_k), int(self.smooth_v), 2.25 if self.pv16 else 448.0, int(self.merge),
+                        *self.layout, None if self.ln is None else self.ln.ctypes.data, float(self.ln_eps),
+                        int(self.pv16))
 
 
 @dataclass
@@ -325,6 +330,11 @@ def layernorm(x: np.ndarray, ln_w: np.ndarray, ln_b: np.ndarray, eps: float = 1e
     for i in range(xr.shape[0]):
         fn(xr[i].ctypes.data, orow[i].ctypes.data, D, _p(w), _p(b), C.c_float(eps))
     return out
+
+
+def round_f16(x: float) -> float:
+    """x rounded to the nearest f16 value (the PvAccum::F16 accumulator), as a float."""
+    return lib().oracle_round_f16(float(x))
 
 
 def log2_count(n: int) -> float:

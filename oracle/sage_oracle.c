@@ -115,6 +115,19 @@ int oracle_s8(float x) {
 
 /* The reference's NVIDIA-fragment key permutation (reference.rs:74-76),
  * kept for its known-answer test (tests.rs:68-83) only. */
+/* Pinned: numpy's float64 -> float16 conversion on random, tie, subnormal and
+ * overflow values (tests/test_oracle_codecs.py). */
+double oracle_round_f16(double x) {
+    if (x == 0.0 || !isfinite(x)) return x;
+    int e;
+    frexp(x, &e);             /* |x| in [2^(e-1), 2^e) */
+    int q = e - 11;           /* f16 keeps 11 significant bits ... */
+    if (q < -24) q = -24;     /* ... down to the subnormal quantum 2^-24 */
+    const double s = ldexp(1.0, q);
+    const double r = rint(x / s) * s; /* exact scaling; rint rounds ties to even */
+    return fabs(r) > 65504.0 ? copysign(INFINITY, x) : r;
+}
+
 int oracle_vpos_ref(int k) { return ((k >> 1) & 3) * 4 + ((k >> 3) << 1) + (k & 1); }
 
 void oracle_decode16(const uint16_t* in, float* out, size_t n, int dtype) {
@@ -675,7 +688,10 @@ static inline float ex2f_cr(float x) { return (float)exp2((double)x); }
  *   then mnew = max(m, fmaf(max x, sc, xoff)); alpha = 2^(m - mnew);
  *   off = (log2(448) - mnew) + xoff; p = 2^fmaf(x, sc, off);
  *   l = fmaf(l, alpha, sum p); P8 = e4m3(p); PV = sum P8*V8 per 64 keys (fp32,
- *   accumulated exactly here); O = fmaf(O, alpha, PV);
+ *   accumulated exactly here; under PvAccum::F16 the f16 accumulator of
+ *   sage_attn.cu:328-333: PV = f16(f16(keys 0..31) + keys 32..63), each
+ *   32-key chunk summed exactly -- the rounding inside NVIDIA's f16-accumulate
+ *   mma is not documented, so that detail is unpinned); O = fmaf(O, alpha, PV);
  *   out = fmaf(O * (1/l), v_scale, v_mean).
  * Masked keys (padding, and j > i when causal) have p = 0.
  * Pinned: closed forms in tests (uniform Q gives the V-code mean; a block of
@@ -764,10 +780,13 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
                     l = fmaf(l, alpha, sum);
                     for (int d = 0; d < D; d++) pv[d] = 0;
                     for (int r = 0; r < ORACLE_KBLOCK; r++) {
-                        if (P[r] == 0.f) continue;
-                        const double p8 = v8f[oracle_f32_to_e4m3(P[r])];
-                        const uint8_t* vr = vb + (size_t)(blk * ORACLE_KBLOCK + r) * D;
-                        for (int d = 0; d < D; d++) pv[d] += p8 * v8f[vr[d]];
+                        if (P[r] != 0.f) {
+                            const double p8 = v8f[oracle_f32_to_e4m3(P[r])];
+                            const uint8_t* vr = vb + (size_t)(blk * ORACLE_KBLOCK + r) * D;
+                            for (int d = 0; d < D; d++) pv[d] += p8 * v8f[vr[d]];
+                        }
+                        if (p->pv16 && (r == 31 || r == 63))
+                            for (int d = 0; d < D; d++) pv[d] = oracle_round_f16(pv[d]);
                     }
                     for (int d = 0; d < D; d++) O[d] = fmaf(O[d], alpha, (float)pv[d]);
                 }

@@ -60,6 +60,9 @@ typedef struct {
      * before anything else reads it; V is never normalised. */
     const float* ln;
     float ln_eps;
+    /* PvAccum::F16 (mod.rs:170-185): v_range is then 2.25 and the emulator
+     * rounds each 64-key block's P.V to f16 after every 32 keys. */
+    int pv16;
 } oracle_problem;
 
 /* LayerNorm of one D-channel row in the prologue kernels' fp32 arithmetic
@@ -91,6 +94,11 @@ int oracle_s8(float x);
 int oracle_vpos_ref(int k);
 
 /* Bulk codec helpers (n elements). */
+/* x rounded to the nearest f16 value (ties to even, subnormals kept, inf past
+ * the largest finite), returned as a double; the f16 accumulator of the
+ * PvAccum::F16 emulation. */
+double oracle_round_f16(double x);
+
 void oracle_decode16(const uint16_t* in, float* out, size_t n, int dtype);
 void oracle_encode16(const float* in, uint16_t* out, size_t n, int dtype);
 void oracle_e4m3_encode(const float* in, uint8_t* out, size_t n);

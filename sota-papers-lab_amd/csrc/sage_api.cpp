@@ -227,9 +227,8 @@ sage_status sage_new(void* stream, uint64_t head_dim, const sage_config* config,
     const sage_config cfg = config ? *config : sage_config_for_head_dim(head_dim);
     sage_status st = sage_tile_validate(&cfg.tile);
     if (st != SAGE_OK) return st;
-    if (cfg.pv_accum == SAGE_PV_F16)
-        return fail(SAGE_ERR_UNSUPPORTED, "FP16 P.V accumulation (PvAccum::F16) is not supported by this build");
-    if (cfg.pv_accum != SAGE_PV_F32) return fail(SAGE_ERR_INVALID, "unknown PvAccum %d", cfg.pv_accum);
+    if (cfg.pv_accum != SAGE_PV_F32 && cfg.pv_accum != SAGE_PV_F16)
+        return fail(SAGE_ERR_INVALID, "unknown PvAccum %d", cfg.pv_accum);
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "current device");
@@ -417,7 +416,9 @@ sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage
     g.kblocks = (int)(plan.tk_pad / SAGE_KBLOCK);
     g.flags = flags;
     g.q_mul = scale * log2e;
-    g.v_range = SAGE_FP8_MAX;
+    // PvAccum::F16 quantises V to +-2.25 (mod.rs:763-766). gfx950's FP8 MFMA
+    // accumulates in fp32 only, so the block partials stay fp32 either way.
+    g.v_range = s->config.pv_accum == SAGE_PV_F16 ? SAGE_PV16_V_RANGE : SAGE_FP8_MAX;
     g.ln_eps = opts->qk_norm_params ? opts->qk_norm_eps : 1e-5f;
     // Merge geometry (mod.rs:727-770): a dense plan is one frame of `tokens`
     // tokens with merge = 1.

@@ -23,7 +23,10 @@ def run(torch, p, q, k, v, out_dtype=None, q_layout="bthd", out_layout="bthd", w
     import spl_sage as S
 
     B, T, H, HK, D = p.batch, p.tokens, p.heads, p.hk, p.head_dim
-    sa = S.SageAttention(None, D)
+    config = None
+    if p.pv16:
+        config = S.Config(S.Config.for_head_dim(D).tile, S.PvAccum.F16)
+    sa = S.SageAttention(None, D, config)
     merge = S.KvMerge.Dense
     if p.merge > 1:
         merge = S.KvMerge.Pool(p.merge, S.FrameLayout(*p.layout))
