@@ -1,0 +1,179 @@
+// CPU tests of the C++ host API (include/spl_sage.hpp) over libsage_hip.so:
+// the reference's host-side tests (sezer-muhammed/sota-papers-lab,
+// platform/spl-nn/src/sage/tests.rs:17-22, 95-190, 245-262) restated against
+// spl_sage:: names, plus the reference's error texts (mod.rs:251-259,
+// 405-440). No GPU call is made. Exit status 0 when every check passes.
+#include <cmath>
+#include <cstdio>
+#include <string>
+#include <type_traits>
+
+#include "spl_sage.hpp"
+
+using namespace spl_sage;
+
+static int failures = 0;
+
+#define CHECK(cond)                                                           \
+    do {                                                                      \
+        if (!(cond)) {                                                        \
+            std::printf("  FAILED %s:%d: %s\n", __FILE__, __LINE__, #cond);   \
+            failures++;                                                       \
+        }                                                                     \
+    } while (0)
+
+// Runs f, which must throw an Error whose status is `status` and whose text
+// contains `text`.
+template <typename F>
+static void expect_error(F f, sage_status status, const char* text, int line) {
+    try {
+        f();
+        std::printf("  FAILED line %d: no error (expected \"%s\")\n", line, text);
+        failures++;
+    } catch (const Error& e) {
+        if (e.status() != status || std::string(e.what()).find(text) == std::string::npos) {
+            std::printf("  FAILED line %d: status %d \"%s\" (expected %d \"%s\")\n", line, (int)e.status(), e.what(),
+                        (int)status, text);
+            failures++;
+        }
+    }
+}
+#define EXPECT_ERROR(expr, status, text) expect_error([&] { expr; }, status, text, __LINE__)
+
+static FrameLayout vggt_layout(std::size_t frames) { return FrameLayout{frames, 17, 21, 32, 0}; }
+
+// tests.rs:17-22: the engine and its workspace move between threads; here,
+// they are move-only owners.
+static void engine_handles_are_move_only() {
+    static_assert(!std::is_copy_constructible<SageAttention>::value, "");
+    static_assert(std::is_nothrow_move_constructible<SageAttention>::value, "");
+    static_assert(!std::is_copy_constructible<Workspace>::value, "");
+    static_assert(std::is_nothrow_move_constructible<Workspace>::value, "");
+}
+
+// tests.rs:95-110: 689 dense keys + 2 x (17 + 6 x 8) pooled.
+static void dense_first_frame_keeps_its_keys() {
+    FrameLayout layout = vggt_layout(3);
+    layout.dense_frames = 1;
+    const Plan plan = Plan::create(Shape{1, 1, 3 * 689}, KvMerge::Pool(4, layout));
+    CHECK(plan.tk == 689 + 2 * 65);
+    CHECK(plan.tk_pad == (plan.tk + 63) / 64 * 64);
+    CHECK(plan.tq_pad == (3 * 689 + 127) / 128 * 128);
+}
+
+// tests.rs:135-150: plan geometry of VGGT-Omega's 200 frames.
+static void vggt_merge_geometry() {
+    const FrameLayout layout = vggt_layout(200);
+    CHECK(layout.tokens_per_frame() == 689);
+    const Shape shape{1, 16, 200 * 689};
+    const Plan dense = Plan::create(shape, KvMerge::Dense());
+    CHECK(dense.tq_pad == 137856 && dense.tk == 137800 && dense.tk_pad == 137856);
+    const Plan m2 = Plan::create(shape, KvMerge::Pool(2, layout));
+    CHECK(m2.tk == 200 * (17 + 11 * 16));
+    const Plan m4 = Plan::create(shape, KvMerge::Pool(4, layout));
+    CHECK(m4.tk == 200 * (17 + 6 * 8));
+    CHECK(layout.merged_per_frame(2) == 17 + 11 * 16 && layout.merged_keys(4) == m4.tk);
+    CHECK(m4.q_tiles() == 137856 / 128 && m4.kblocks() == m4.tk_pad / 64);
+}
+
+// tests.rs:174-190.
+static void plan_rejects_bad_layouts() {
+    const FrameLayout layout = vggt_layout(2);
+    EXPECT_ERROR(Plan::create(Shape{1, 2, 1000}, KvMerge::Pool(2, layout)), SAGE_ERR_INVALID, "");
+    const Shape shape{1, 2, 2 * 689};
+    EXPECT_ERROR(Plan::create(shape, KvMerge::Pool(3, layout)), SAGE_ERR_INVALID, "");
+    Plan::create(shape, KvMerge::Pool(4, layout));
+    EXPECT_ERROR(Plan::create(Shape{1, 2, 0}, KvMerge::Dense()), SAGE_ERR_INVALID, "");
+    // Grouped-query heads must divide the query heads (extension).
+    EXPECT_ERROR(Plan::create(Shape{1, 6, 128, 4}, KvMerge::Dense()), SAGE_ERR_INVALID, "");
+    const Plan gqa = Plan::create(Shape{1, 32, 8192, 8}, KvMerge::Dense());
+    CHECK(gqa.shape.kv() == 8);
+}
+
+// tests.rs:245-262.
+static void strides_cover_the_tensor() {
+    const Shape shape{2, 3, 5};
+    const std::size_t d = 64;
+    CHECK(Strides::bthd(5, 3, d).extent(shape, d) == 2 * 5 * 3 * d);
+    CHECK(Strides::bhtd(5, 3, d).extent(shape, d) == 2 * 3 * 5 * d);
+    // A packed QKV view starting at V's offset ends at the buffer's end.
+    CHECK(Strides::packed_qkv(5, 3, d).extent(shape, d) + 2 * 3 * d == 2 * 5 * 3 * 3 * d);
+    EXPECT_ERROR(Strides::bthd(5, 3, 60).check("x"), SAGE_ERR_INVALID, "x");
+    Strides::bthd(5, 3, 64).check("x");
+}
+
+// mod.rs:116-201: this build's tile menu and the default config.
+static void tiles_and_config() {
+    for (std::size_t d : {64, 128}) {
+        const Config c = Config::for_head_dim(d);
+        CHECK(c.pv_accum == PvAccum::F32);
+        c.tile.validate();
+        CHECK(c.tile.rows() == 128);
+    }
+    EXPECT_ERROR((Tile{8, 1, 2}.validate()), SAGE_ERR_INVALID, "unsupported sage tile");
+}
+
+// mod.rs:905-910 and the benchmark's operation counts.
+static void flops_counts_the_pairs() {
+    const Plan c2 = Plan::create(Shape{2, 32, 4096}, KvMerge::Dense());
+    CHECK(flops(c2, 128) == 4.0 * 2 * 32 * 4096.0 * 4096.0 * 128);
+    const Plan c3 = Plan::create(Shape{1, 32, 16384}, KvMerge::Dense());
+    CHECK(flops(c3, 128, true) == 2.0 * 32 * 128 * 16384.0 * 16385.0);
+    // Merged keys count as keys.
+    FrameLayout layout = vggt_layout(2);
+    const Plan m = Plan::create(Shape{1, 1, 2 * 689}, KvMerge::Pool(4, layout));
+    CHECK(flops(m, 64) == 4.0 * (2 * 689.0) * (double)m.tk * 64);
+}
+
+// The v8 key order is a permutation of the 64 keys of a block.
+static void v8_positions_are_a_permutation() {
+    int seen[64] = {};
+    for (int k = 0; k < 64; k++) {
+        const int p = v8_position(k);
+        CHECK(p >= 0 && p < 64);
+        if (p >= 0 && p < 64) seen[p]++;
+    }
+    for (int p = 0; p < 64; p++) CHECK(seen[p] == 1);
+    CHECK(v8_position(64) == -1 && v8_position(-1) == -1);
+}
+
+// Options map onto the C struct as the reference's defaults say (mod.rs:326-335).
+static void options_defaults() {
+    const sage_options o = Options{}.raw();
+    CHECK(o.smooth_k == 1 && o.smooth_v == 1 && o.has_softmax_scale == 0 && o.qk_norm_params == nullptr &&
+          o.causal == 0);
+    Options with;
+    with.softmax_scale = 0.125f;
+    with.qk_norm = QkNorm{reinterpret_cast<const float*>(16), 256, 1e-6f};
+    const sage_options w = with.raw();
+    CHECK(w.has_softmax_scale == 1 && w.softmax_scale == 0.125f && w.qk_norm_len == 256 && w.qk_norm_eps == 1e-6f);
+}
+
+int main() {
+    struct {
+        const char* name;
+        void (*fn)();
+    } tests[] = {
+        {"engine_handles_are_move_only", engine_handles_are_move_only},
+        {"dense_first_frame_keeps_its_keys", dense_first_frame_keeps_its_keys},
+        {"vggt_merge_geometry", vggt_merge_geometry},
+        {"plan_rejects_bad_layouts", plan_rejects_bad_layouts},
+        {"strides_cover_the_tensor", strides_cover_the_tensor},
+        {"tiles_and_config", tiles_and_config},
+        {"flops_counts_the_pairs", flops_counts_the_pairs},
+        {"v8_positions_are_a_permutation", v8_positions_are_a_permutation},
+        {"options_defaults", options_defaults},
+    };
+    for (auto& t : tests) {
+        const int before = failures;
+        try {
+            t.fn();
+        } catch (const std::exception& e) {
+            std::printf("  FAILED: unexpected exception: %s\n", e.what());
+            failures++;
+        }
+        std::printf("%s %s\n", failures == before ? "ok" : "FAIL", t.name);
+    }
+    std::printf("%d failure(s)\n", failures);
+    return failures ? 1 : 0;
+}
