@@ -349,11 +349,14 @@ class Workspace:
         self._h = handle
         self._plan = plan
         self.head_dim = head_dim
+        # Bound now: at interpreter exit the module's globals may be gone before __del__ runs.
+        self._destroy = lib().sage_workspace_destroy
 
     def __del__(self):
         h, self._h = getattr(self, "_h", None), None
-        if h:
-            lib().sage_workspace_destroy(h)
+        destroy = getattr(self, "_destroy", None)
+        if h and destroy is not None:
+            destroy(h)
 
     def plan(self) -> Plan:
         return self._plan
@@ -421,6 +424,7 @@ class SageAttention:
         _check(lib().sage_new(_stream_handle(stream), head_dim, cfg, C.byref(h)))
         self._h = h.value
         self._stream = stream
+        self._destroy = lib().sage_destroy
 
     @classmethod
     def new(cls, stream, head_dim: int) -> "SageAttention":
@@ -432,8 +436,9 @@ class SageAttention:
 
     def __del__(self):
         h, self._h = getattr(self, "_h", None), None
-        if h:
-            lib().sage_destroy(h)
+        destroy = getattr(self, "_destroy", None)
+        if h and destroy is not None:
+            destroy(h)
 
     def head_dim(self) -> int:
         return lib().sage_head_dim(self._h)
