@@ -114,6 +114,22 @@ def test_plan_rejects_bad_layouts(S):
         S.Plan.new(S.Shape(1, 2, 0))
 
 
+def test_plan_range_checks(S):
+    """mod.rs:406-439: an empty patch grid, and every count the kernels index
+    with i32 (padded queries, padded keys, batch x heads) refused with the
+    reference's texts."""
+    with pytest.raises(S.SageError, match="KV merge needs a patch grid"):
+        S.Plan.new(S.Shape(1, 1, 10), S.KvMerge.Pool(2, S.FrameLayout(2, 5, 0, 4, 0)))
+    with pytest.raises(S.SageError, match="padded queries = 2147483648 does not fit in i32"):
+        S.Plan.new(S.Shape(1, 1, 2**31 - 5))
+    with pytest.raises(S.SageError, match="batch .* heads = 2147483648 does not fit in i32"):
+        S.Plan.new(S.Shape(2**16, 2**15, 128))
+    # The largest sizes that fit are accepted.
+    p = S.Plan.new(S.Shape(1, 1, 2**31 - 128))
+    assert p.tq_pad == 2**31 - 128 and p.tk_pad == 2**31 - 128
+    S.Plan.new(S.Shape(2**16, 2**15 - 1, 128))
+
+
 def test_plan_padding_and_tails(S):
     """mod.rs:431-434: tq_pad to 128, tk_pad to 64; the C5 tail shape."""
     p = S.Plan.new(S.Shape(1, 48, 17776))
