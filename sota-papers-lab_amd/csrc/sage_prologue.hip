@@ -258,6 +258,21 @@ __global__ __launch_bounds__(4 * D) void sage_finalize(const float* __restrict__
     }
 }
 
+// E4M3 codes of one key's 8 channels (ch * 8 .. + 7) into the transposed V
+// tile: channel row r, byte v8_position(kl). Row r keeps its 16 dwords
+// XOR-permuted by r >> 3 (= ch): the channel groups of a wave write rows
+// 512 bytes apart, which would all fall in one LDS bank, and the permutation
+// spreads them over 16 (D = 128) or 8 (D = 64) banks; the copy to HBM undoes it.
+__device__ __forceinline__ void put_v(uint8_t* vt, int ch, int kl, const float* vq) {
+    const int pos = v8_position(kl) ^ ((ch & 15) << 2);
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const uint32_t two = e4m3_pair(vq[e], vq[e + 1]);
+        vt[(ch * 8 + e) * KBLOCK + pos] = (uint8_t)two;
+        vt[(ch * 8 + e + 1) * KBLOCK + pos] = (uint8_t)(two >> 8);
+    }
+}
+
 // sage_quant.cu:238-319 (sg_quant_kv): K - mean -> INT8 per block,
 // (V - mean) / scale -> E4M3, V stored [block][channel][v8_position(key)].
 // A merged key sums its members in order from 0.0f and takes
@@ -311,15 +326,15 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
             unpack8(kraw[i], fk, f16);
             unpack8(vraw[i], fv, f16);
             if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
-            const int pos = v8_position(kl);
+            float vq[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 // The reference sums the (one) member from 0.0f first: -0 becomes +0.
                 kv[i][e] = ok ? (fk[e] + 0.0f) - mk[e] : 0.f;
                 amax = fmaxf(amax, fabsf(kv[i][e]));
-                const float vq = ok ? ((fv[e] + 0.0f) - mv[e]) * iv[e] : 0.f;
-                vt[(ch * 8 + e) * KBLOCK + pos] = (uint8_t)e4m3_code(vq);
+                vq[e] = ok ? ((fv[e] + 0.0f) - mv[e]) * iv[e] : 0.f;
             }
+            put_v(vt, ch, kl, vq);
         }
     } else {
         __syncthreads();
@@ -350,14 +365,14 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
                 }
             }
             const float rc = cnt > 0 ? 1.0f / (float)cnt : 0.f;
-            const int pos = v8_position(kl);
+            float vq[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 kv[i][e] = ok ? __builtin_fmaf(ks[e], rc, -mk[e]) : 0.f;
                 amax = fmaxf(amax, fabsf(kv[i][e]));
-                const float vq = ok ? __builtin_fmaf(vs[e], rc, -mv[e]) * iv[e] : 0.f;
-                vt[(ch * 8 + e) * KBLOCK + pos] = (uint8_t)e4m3_code(vq);
+                vq[e] = ok ? __builtin_fmaf(vs[e], rc, -mv[e]) * iv[e] : 0.f;
             }
+            put_v(vt, ch, kl, vq);
         }
     }
     amax = wave_max(amax);
@@ -376,9 +391,18 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
         *reinterpret_cast<uint2*>(k8 + (bhk * g.tk_pad + blk * KBLOCK + kl) * D + ch * 8) = w;
     }
     if (tid == 0) k_scale[bhk * g.kblocks + blk] = km * (1.0f / 127.0f);
+    // Channel row r of the tile, un-permuting its dwords (see put_v).
     uint8_t* vo = v8 + (bhk * g.kblocks + blk) * (long long)(D * KBLOCK);
-    for (int c = tid; c < D * KBLOCK / 16; c += 256)
-        reinterpret_cast<uint4*>(vo)[c] = reinterpret_cast<const uint4*>(vt)[c];
+    for (int c = tid; c < D * KBLOCK / 16; c += 256) {
+        const int r = c >> 2, sw = (r >> 3) & 15;  // row r, 16-byte chunk c & 3
+        const uint32_t* row = reinterpret_cast<const uint32_t*>(vt + r * KBLOCK);
+        uint4 w;
+        w.x = row[(4 * (c & 3) + 0) ^ sw];
+        w.y = row[(4 * (c & 3) + 1) ^ sw];
+        w.z = row[(4 * (c & 3) + 2) ^ sw];
+        w.w = row[(4 * (c & 3) + 3) ^ sw];
+        reinterpret_cast<uint4*>(vo)[c] = w;
+    }
     // The merge bias depends on the key alone (sage_quant.cu:321-325).
     if (g.merge > 1 && b == 0 && hk == 0 && tid < KBLOCK) {
         const int j = blk * KBLOCK + tid;
