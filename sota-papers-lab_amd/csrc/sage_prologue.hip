@@ -2,10 +2,11 @@
 // scale per 16 rows), INT8 K (one scale per 64 keys), FP8 E4M3 V (one scale
 // per channel). Three HBM-bound launches:
 //
-//   sage_prep      grid (q_tiles, kv_heads, batch): per 128-token tile, the
-//                  partial K sum, V sum, V min, V max of every channel, and
-//                  INT8 Q of the `group` query heads that share the KV head
-//                  (Q and K rows LayerNormed first under QK LayerNorm)
+//   sage_prep      grid (2 q_tiles, kv_heads, batch): per 128-token tile, one
+//                  workgroup writes the partial K sum, V sum, V min, V max of
+//                  every channel, another the INT8 Q of the `group` query
+//                  heads that share the KV head (Q and K rows LayerNormed
+//                  first under QK LayerNorm)
 //   sage_finalize  grid (kv_heads, batch): K mean, V mean, V scale, 1/V scale
 //   sage_quant_kv  grid (kblocks, kv_heads, batch): smoothed INT8 K and FP8 V,
 //                  V transposed per 64-key block into the MFMA operand order;
@@ -66,27 +67,23 @@ __device__ __forceinline__ void layernorm8(float* x, const float* __restrict__ w
     for (int e = 0; e < 8; e++) x[e] = __builtin_fmaf((x[e] - mean) * rstd, w[ch * 8 + e], bias[ch * 8 + e]);
 }
 
-// sage_quant.cu:59-160 (sg_prep). Under QK LayerNorm (LN, the F_LN_Q and
-// F_LN_K flags together as the reference sets them) every K row is normalised
-// before the statistics read it and every Q row before its amax; the LN-free
-// instantiation keeps the dense kernel's registers.
+// sage_quant.cu:59-160 (sg_prep), in two roles. Under QK LayerNorm (LN, the
+// F_LN_Q and F_LN_K flags together as the reference sets them) every K row is
+// normalised before the statistics read it and every Q row before its amax;
+// the LN-free instantiation keeps the dense kernel's registers.
+
+// K and V channel statistics of one 128-token tile (sage_quant.cu:73-80,
+// 97-107, 129-159): the tile's partial K sum, V sum, V min and V max.
 template <int D, bool LN>
-__global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                                                 const uint16_t* __restrict__ v, const float* __restrict__ ln,
-                                                 int8_t* __restrict__ q8, float* __restrict__ q_scale,
-                                                 float* __restrict__ part, Geom g) {
+__device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                           const float* __restrict__ ln, float* __restrict__ part, const Geom& g,
+                                           int tile, int hk, int b, float (*red)[4][D]) {
     constexpr int CH = D / 8;        // 16-byte chunks per head row
     constexpr int TPI = 256 / CH;    // tokens per iteration
     constexpr int NI = QTILE / TPI;  // iterations
-    const int tile = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, ch = tid % CH, slot = tid / CH;
     const bool f16 = g.flags & F_IN_F16;
     const long long bhk = (long long)b * g.kv_heads + hk;
-
-    __shared__ unsigned gmax[QTILE / QGROUP];
-    __shared__ float red[8][4][D];
-
-    // K and V channel statistics of this tile's tokens.
     float ks[8], vs[8], vmn[8], vmx[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
@@ -152,8 +149,19 @@ __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q,
         }
         part[((bhk * g.q_tiles + tile) * 4 + stat) * D + d] = r;
     }
+}
 
-    // INT8 Q of every query head that reads this KV head (sage_quant.cu:85-127).
+// INT8 Q of one 128-token tile of every query head that reads KV head hk
+// (sage_quant.cu:85-127).
+template <int D, bool LN>
+__device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const float* __restrict__ ln,
+                                        int8_t* __restrict__ q8, float* __restrict__ q_scale, const Geom& g,
+                                        int tile, int hk, int b, unsigned* gmax) {
+    constexpr int CH = D / 8;
+    constexpr int TPI = 256 / CH;
+    constexpr int NI = QTILE / TPI;
+    const int tid = threadIdx.x, ch = tid % CH, slot = tid / CH;
+    const bool f16 = g.flags & F_IN_F16;
     for (int gi = 0; gi < g.group; gi++) {
         const int h = hk * g.group + gi;
         const long long bh = (long long)b * g.heads + h;
@@ -200,6 +208,23 @@ __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q,
                 __uint_as_float(gmax[tid]) * (1.0f / 127.0f) * g.q_mul;
         __syncthreads();
     }
+}
+
+// Two workgroups a tile: even blockIdx.x the K/V statistics, odd the INT8 Q.
+// The reference's one thread block does both in turn; split, the two streams
+// of loads overlap across workgroups.
+template <int D, bool LN>
+__global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                 const uint16_t* __restrict__ v, const float* __restrict__ ln,
+                                                 int8_t* __restrict__ q8, float* __restrict__ q_scale,
+                                                 float* __restrict__ part, Geom g) {
+    __shared__ unsigned gmax[QTILE / QGROUP];
+    __shared__ float red[8][4][D];
+    const int tile = (int)blockIdx.x >> 1, hk = blockIdx.y, b = blockIdx.z;
+    if (blockIdx.x & 1)
+        tile_q8<D, LN>(q, ln, q8, q_scale, g, tile, hk, b, gmax);
+    else
+        tile_stats<D, LN>(k, v, ln, part, g, tile, hk, b, red);
 }
 
 // sage_quant.cu:163-206 (sg_finalize): even and odd tiles folded separately.
@@ -414,7 +439,7 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
 template <int D, bool LN>
 static hipError_t launch_prologue_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ln,
                                     const PrologueBufs& w, const Geom& g, hipStream_t s) {
-    hipLaunchKernelGGL((sage_prep<D, LN>), dim3(g.q_tiles, g.kv_heads, g.batch), dim3(256), 0, s, q, k, v, ln, w.q8,
+    hipLaunchKernelGGL((sage_prep<D, LN>), dim3(2 * g.q_tiles, g.kv_heads, g.batch), dim3(256), 0, s, q, k, v, ln, w.q8,
                        w.q_scale, w.part, g);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
