@@ -126,6 +126,57 @@ def cpu_baseline(q, k, v, cfg: int, budget_s: float = 12.0) -> dict:
     }
 
 
+def vggt_bench(args, torch, S) -> int:
+    """The reference's gpu_bench (tests.rs:817-990): VGGT-Omega's global
+    attention at 512x336, B1 H16 D64, `frames` frames of 689 tokens, dense or
+    KV-merged (stride 2 or 4, every frame merged as in vggt_layout), with the
+    PvAccum and QK-norm options. Prints one JSON line: prologue and attention
+    times, attention TOPS over the merged keys (mod.rs:905-910)."""
+    B, H, D, frames = 1, 16, 64, args.frames
+    layout = S.FrameLayout(frames, 17, 21, 32, 0)
+    N = frames * layout.tokens_per_frame()
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn((B, N, H, D), generator=g, device="cuda").to(torch.bfloat16)
+    k = (torch.randn((B, N, H, D), generator=g, device="cuda")
+         + 2.0 * torch.randn((H, D), generator=g, device="cuda")).to(torch.bfloat16)
+    v = torch.randn((B, N, H, D), generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+    cfg = S.Config(S.Config.for_head_dim(D).tile, S.PvAccum.F16 if args.pv16 else S.PvAccum.F32)
+    sa = S.SageAttention(stream, D, cfg)
+    merge = S.KvMerge.Pool(args.merge, layout) if args.merge > 1 else S.KvMerge.Dense
+    ws = sa.workspace(S.Shape(B, H, N), merge)
+    qk_norm = None
+    if args.qk_norm:
+        lnp = torch.cat([1 + 0.5 * torch.randn(D, generator=g, device="cuda"), 0.8 * torch.randn(D, generator=g, device="cuda"),
+                         1 + 0.5 * torch.randn(D, generator=g, device="cuda"), 0.8 * torch.randn(D, generator=g, device="cuda")])
+        qk_norm = S.QkNorm(lnp.float().contiguous(), 1e-5)
+    opts = S.Options(qk_norm=qk_norm)
+    qt, kt, vt, ot = S.Tensor(q), S.Tensor(k), S.Tensor(v), S.TensorMut(out)
+    plan = ws.plan()
+    ops = S.flops(plan, D)
+    sa.prepare(ws, qt, kt, vt, opts)
+    for _ in range(args.warmup):
+        sa.attend(ws, ot)
+    torch.cuda.synchronize()
+    reps = max(args.steps, 5)
+    attn_ms = time_events(torch, stream, lambda: sa.attend(ws, ot), reps)
+    prep_ms = time_events(torch, stream, lambda: sa.prepare(ws, qt, kt, vt, opts), reps)
+    step_ms = time_events(torch, stream, lambda: sa.forward(ws, qt, kt, vt, ot, opts), reps)
+    regs, spill = sa.attn_resources()
+    mode = ("dense" if args.merge == 1 else f"merge{args.merge}") + ("_pv16" if args.pv16 else "") + \
+        ("_qknorm" if args.qk_norm else "")
+    attn_tops = ops / (attn_ms * 1e-3) / 1e12
+    print(json.dumps({
+        "workload": "VGGT-Omega global attention (reference gpu_bench)", "mode": mode, "frames": frames,
+        "heads": H, "head_dim": D, "tokens": N, "keys": plan.tk, "prologue_ms": round(prep_ms, 4),
+        "attention_ms": round(attn_ms, 4), "attention_tops": round(attn_tops, 1),
+        "attention_frac_of_peak": round(attn_tops / VENDOR_PEAK_TOPS, 4), "step_ms": round(step_ms, 4),
+        "step_tops": round(ops / (step_ms * 1e-3) / 1e12, 1), "vgprs_dense_kernel": regs, "spill": spill,
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -135,6 +186,13 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-peak", action="store_true", help="skip the MFMA peak probes")
+    ap.add_argument("--vggt", action="store_true",
+                    help="instead of the headline line: the reference's gpu_bench workload (tests.rs:817-990), "
+                         "VGGT-Omega global attention, 689-token frames (17 special + 21x32 patches), 16 heads of 64")
+    ap.add_argument("--frames", type=int, default=200, help="--vggt: frames (200 = 137800 tokens)")
+    ap.add_argument("--merge", type=int, default=1, choices=[1, 2, 4], help="--vggt: KV merge stride (1 = dense)")
+    ap.add_argument("--pv16", action="store_true", help="--vggt: PvAccum::F16")
+    ap.add_argument("--qk-norm", action="store_true", help="--vggt: fused QK LayerNorm")
     ap.add_argument("--only", choices=["attend", "prepare", "copy"],
                     help="profiling mode: run only this kernel group --steps times and print its timing "
                          "(copy: a plain 512 MiB device copy, the reference for HBM byte counters)")
@@ -148,6 +206,8 @@ def main() -> int:
     import spl_sage as S
 
     torch.cuda.set_device(0)
+    if args.vggt:
+        return vggt_bench(args, torch, S)
     if args.only == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
