@@ -189,7 +189,8 @@ double sage_flops(const sage_plan* plan, uint64_t head_dim, int32_t causal);
 /* Strides::check (mod.rs:251-259); `what` names the tensor in the message. */
 sage_status sage_strides_check(const sage_strides* s, const char* what);
 
-/* Strides::extent (mod.rs:244-249) for `heads` heads. */
+/* Strides::extent (mod.rs:244-249) for `heads` heads; UINT64_MAX when the
+ * extent does not fit 64 bits. */
 uint64_t sage_strides_extent(const sage_strides* s, uint64_t batch, uint64_t tokens, uint64_t heads,
                              uint64_t head_dim);
 

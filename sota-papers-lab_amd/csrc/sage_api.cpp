@@ -131,6 +131,12 @@ sage_status sage_plan_new(const sage_shape* shape, const sage_kv_merge* merge, s
     const sage_shape& s = *shape;
     if (s.batch == 0 || s.heads == 0 || s.tokens == 0)
         return fail(SAGE_ERR_INVALID, "empty attention shape %s", shape_dbg(s).c_str());
+    // Counts so large that padding or a product would wrap 64 bits cannot fit the
+    // i32 indexing either; report them with the same text as the checks below.
+    if (s.tokens > 0x7fffffffull)
+        return fail(SAGE_ERR_INVALID, "padded queries = %llu does not fit in i32", (u64)s.tokens);
+    if (s.batch > 0x7fffffffull || s.heads > 0x7fffffffull)
+        return fail(SAGE_ERR_INVALID, "batch × heads = %llu × %llu does not fit in i32", (u64)s.batch, (u64)s.heads);
     const uint64_t hk = kv_heads_of(s);
     if (s.heads % hk != 0)
         return fail(SAGE_ERR_INVALID, "%llu query heads are not a multiple of %llu KV heads", (u64)s.heads, (u64)hk);
@@ -181,7 +187,13 @@ sage_status sage_strides_check(const sage_strides* s, const char* what) {
 uint64_t sage_strides_extent(const sage_strides* s, uint64_t batch, uint64_t tokens, uint64_t heads,
                              uint64_t head_dim) {
     if (!s || batch == 0 || tokens == 0 || heads == 0) return 0;
-    return (batch - 1) * s->batch + (tokens - 1) * s->token + (heads - 1) * s->head + head_dim;
+    // A view whose extent does not fit 64 bits needs more than any buffer holds.
+    uint64_t a, b, c, e;
+    if (__builtin_mul_overflow(batch - 1, s->batch, &a) || __builtin_mul_overflow(tokens - 1, s->token, &b) ||
+        __builtin_mul_overflow(heads - 1, s->head, &c) || __builtin_add_overflow(a, b, &e) ||
+        __builtin_add_overflow(e, c, &e) || __builtin_add_overflow(e, head_dim, &e))
+        return UINT64_MAX;
+    return e;
 }
 
 // This build's tile menu: 4 wave64s of one 32-query MFMA tile each, two K/V

@@ -124,10 +124,23 @@ def test_plan_range_checks(S):
         S.Plan.new(S.Shape(1, 1, 2**31 - 5))
     with pytest.raises(S.SageError, match="batch .* heads = 2147483648 does not fit in i32"):
         S.Plan.new(S.Shape(2**16, 2**15, 128))
+    # Sizes whose padding or product would wrap 64 bits are refused, not wrapped.
+    with pytest.raises(S.SageError, match="padded queries"):
+        S.Plan.new(S.Shape(1, 1, 2**64 - 1))
+    with pytest.raises(S.SageError, match="batch .* heads"):
+        S.Plan.new(S.Shape(2**40, 2**30, 128))
     # The largest sizes that fit are accepted.
     p = S.Plan.new(S.Shape(1, 1, 2**31 - 128))
     assert p.tq_pad == 2**31 - 128 and p.tk_pad == 2**31 - 128
     S.Plan.new(S.Shape(2**16, 2**15 - 1, 128))
+
+
+def test_extent_does_not_wrap(S):
+    """Strides whose extent would wrap 64 bits report the largest extent, so a
+    view with them can never pass the length check."""
+    shape = S.Shape(1, 1, 5)
+    assert S.Strides(8, 2**62, 8).extent(shape, 64) == 2**64 - 1
+    assert S.Strides(8, 2**61, 8).extent(shape, 64) == 4 * 2**61 + 64
 
 
 def test_plan_padding_and_tails(S):
