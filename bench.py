@@ -9,6 +9,13 @@ synthetic inputs already resident in HBM. `value` is whole-step throughput in
 TOPS (4*B*H*N^2*D algorithmic ops per step, the reference's `flops`,
 mod.rs:905-910); `attention` reports the attention kernel alone, like the
 reference's attn_tops (tests.rs:968-971). One GPU only.
+
+    python bench.py --vggt [--frames 200] [--merge 1|2|4] [--pv16] [--qk-norm]
+
+prints, instead of the headline line, the reference's own gpu_bench workload
+(tests.rs:817-990: VGGT-Omega global attention, B1 H16 D64, 689-token frames)
+in the chosen mode. `--only attend|prepare|copy` times one kernel group (for
+the profiler).
 """
 from __future__ import annotations
 
