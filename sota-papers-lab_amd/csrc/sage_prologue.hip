@@ -20,13 +20,33 @@
 // fold. A 256-thread workgroup here is four wave64s; each 32-lane half of a
 // wave plays one of the reference's warps, so the same partials meet in the
 // same order.
+//
+// Cache policy: sage_quant_kv re-reads the K and V that sage_prep read, and
+// MI355X's memory-side cache can hold much of them in between. Everything
+// read or written exactly once goes around it (non-temporal): the Q load and
+// the q8, k8 and v8 stores. The attention kernel shares its K/V tiles through
+// L2, not through that cache.
 #include "sage_device.hpp"
 #include "sage_internal.hpp"
 
 namespace sage {
 
+typedef unsigned nt_u2 __attribute__((ext_vector_type(2)));
+typedef unsigned nt_u4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ uint4 load16(const uint16_t* p, bool ok) {
     return ok ? *reinterpret_cast<const uint4*>(p) : make_uint4(0, 0, 0, 0);
+}
+__device__ __forceinline__ uint4 load16_once(const uint16_t* p, bool ok) {
+    if (!ok) return make_uint4(0, 0, 0, 0);
+    const nt_u4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store8_once(void* p, uint2 w) {
+    __builtin_nontemporal_store(nt_u2{w.x, w.y}, reinterpret_cast<nt_u2*>(p));
+}
+__device__ __forceinline__ void store16_once(void* p, uint4 w) {
+    __builtin_nontemporal_store(nt_u4{w.x, w.y, w.z, w.w}, reinterpret_cast<nt_u4*>(p));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -171,7 +191,7 @@ __device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const fl
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int tok = tile * QTILE + slot + i * TPI;
-            qraw[i] = load16(q + b * g.q_sb + (long long)tok * g.q_st + h * g.q_sh + ch * 8, tok < g.tokens);
+            qraw[i] = load16_once(q + b * g.q_sb + (long long)tok * g.q_st + h * g.q_sh + ch * 8, tok < g.tokens);
         }
         float qv[NI][8];
 #pragma unroll
@@ -201,7 +221,7 @@ __device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const fl
             uint2 w;
             w.x = s8x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
             w.y = s8x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
-            *reinterpret_cast<uint2*>(q8 + (bh * g.tq_pad + tile * QTILE + tl) * D + ch * 8) = w;
+            store8_once(q8 + (bh * g.tq_pad + tile * QTILE + tl) * D + ch * 8, w);
         }
         if (tid < QTILE / QGROUP)
             q_scale[bh * (g.tq_pad / QGROUP) + tile * (QTILE / QGROUP) + tid] =
@@ -413,7 +433,7 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
         uint2 w;
         w.x = s8x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
         w.y = s8x4(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
-        *reinterpret_cast<uint2*>(k8 + (bhk * g.tk_pad + blk * KBLOCK + kl) * D + ch * 8) = w;
+        store8_once(k8 + (bhk * g.tk_pad + blk * KBLOCK + kl) * D + ch * 8, w);
     }
     if (tid == 0) k_scale[bhk * g.kblocks + blk] = km * (1.0f / 127.0f);
     // Channel row r of the tile, un-permuting its dwords (see put_v).
@@ -426,7 +446,7 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
         w.y = row[(4 * (c & 3) + 1) ^ sw];
         w.z = row[(4 * (c & 3) + 2) ^ sw];
         w.w = row[(4 * (c & 3) + 3) ^ sw];
-        reinterpret_cast<uint4*>(vo)[c] = w;
+        store16_once(reinterpret_cast<uint4*>(vo) + c, w);
     }
     // The merge bias depends on the key alone (sage_quant.cu:321-325).
     if (g.merge > 1 && b == 0 && hk == 0 && tid < KBLOCK) {
