@@ -217,7 +217,8 @@ void* sage_stream(const sage_attention* s);                  /* mod.rs:636-638 *
 sage_status sage_attn_resources(const sage_attention* s, int32_t* regs, int32_t* spill, int32_t* lds);
 
 /* SageAttention::workspace (mod.rs:648-670): allocates (and zero-fills) the
- * buffers for `shape` and `merge`. */
+ * buffers for `shape` and `merge`. A shape whose buffers would need more than
+ * 2^62 bytes in total is refused (SAGE_ERR_INVALID) before any allocation. */
 sage_status sage_workspace_new(const sage_attention* s, const sage_shape* shape, const sage_kv_merge* merge,
                            sage_workspace** out);
 void sage_workspace_destroy(sage_workspace* ws);

@@ -149,9 +149,15 @@ sage_status sage_plan_new(const sage_shape* shape, const sage_kv_merge* merge, s
         const sage_frame_layout& l = merge->layout;
         if (l.grid_h == 0 || l.grid_w == 0)
             return fail(SAGE_ERR_INVALID, "KV merge needs a patch grid: %s", layout_dbg(l).c_str());
-        if (l.frames * tokens_per_frame(l) != s.tokens)
+        // A layout whose token count wraps 64 bits covers more tokens than any sequence.
+        uint64_t cells, per_frame, covered;
+        if (__builtin_mul_overflow(l.grid_h, l.grid_w, &cells) || __builtin_add_overflow(cells, l.special, &per_frame) ||
+            __builtin_mul_overflow(l.frames, per_frame, &covered))
+            return fail(SAGE_ERR_INVALID, "frame layout %s covers more than 2^64 tokens, the sequence has %llu",
+                        layout_dbg(l).c_str(), (u64)s.tokens);
+        if (covered != s.tokens)
             return fail(SAGE_ERR_INVALID, "frame layout %s covers %llu tokens, the sequence has %llu",
-                        layout_dbg(l).c_str(), (u64)(l.frames * tokens_per_frame(l)), (u64)s.tokens);
+                        layout_dbg(l).c_str(), (u64)covered, (u64)s.tokens);
         tk = merged_keys(l, merge->stride);
     }
     sage_plan p{};
@@ -287,18 +293,31 @@ sage_status sage_workspace_new(const sage_attention* s, const sage_shape* shape,
     sage_status st = sage_plan_new(shape, merge ? merge : &dense, &plan);
     if (st != SAGE_OK) return st;
     const uint64_t b = plan.shape.batch, h = plan.shape.heads, hk = plan.shape.kv_heads, d = s->head_dim;
+    // Every buffer size, and their sum in bytes, must be addressable: the
+    // plan's i32 checks bound each factor, not their products. The code
+    // buffers and the partials dominate; capping them at 2^62 bytes keeps the
+    // scale, statistics and bias buffers' small additions from wrapping too.
+    uint64_t n_q8, n_k8, n_part, total;
+    const bool wraps = __builtin_mul_overflow(b * h, plan.tq_pad, &n_q8) || __builtin_mul_overflow(n_q8, d, &n_q8) ||
+                       __builtin_mul_overflow(b * hk, plan.tk_pad, &n_k8) || __builtin_mul_overflow(n_k8, d, &n_k8) ||
+                       __builtin_mul_overflow(b * hk * 4 * d, plan.tq_pad / SAGE_QTILE, &n_part) ||
+                       __builtin_mul_overflow(n_part, (uint64_t)4, &total) ||
+                       __builtin_add_overflow(total, n_q8, &total) || __builtin_add_overflow(total, n_k8, &total) ||
+                       __builtin_add_overflow(total, n_k8, &total) || total > (1ull << 62);
+    if (wraps)
+        return fail(SAGE_ERR_INVALID, "sage workspace for %s is too large to address", shape_dbg(*shape).c_str());
     sage_workspace* w = new sage_workspace;
     w->plan = plan;
     w->head_dim = d;
     w->device = s->device;
-    w->n_q8 = b * h * plan.tq_pad * d;
+    w->n_q8 = n_q8;
     w->n_q_scale = b * h * plan.tq_pad / SAGE_QGROUP;
-    w->n_k8 = b * hk * plan.tk_pad * d;
+    w->n_k8 = n_k8;
     w->n_k_scale = b * hk * plan.tk_pad / SAGE_KBLOCK;
-    w->n_v8 = b * hk * plan.tk_pad * d;
+    w->n_v8 = n_k8;
     w->n_stats = b * hk * 4 * d;
     w->n_kbias = plan.tk_pad;
-    w->n_part = b * hk * (plan.tq_pad / SAGE_QTILE) * 4 * d;
+    w->n_part = n_part;
     struct {
         void** p;
         uint64_t bytes;

@@ -33,6 +33,17 @@ def test_head_dim_is_64_or_128(ctx):
     assert _status(e) == 1
 
 
+def test_workspace_sizes_do_not_wrap(ctx):
+    """A plan whose every count fits i32 can still need more than 2^64 bytes of
+    codes (here 2^31 - 32768 heads of 2^30 padded queries at head dim 64): the
+    workspace is refused before any allocation, not sized by a wrapped product."""
+    S = ctx[0]
+    sa = ctx[2]
+    with pytest.raises(S.SageError, match="sage workspace for .* is too large to address") as e:
+        sa.workspace(S.Shape(32768, 65535, 2**30))
+    assert _status(e) == 1
+
+
 def test_attend_before_prepare(ctx):
     S, torch, sa, ws, x, out = ctx
     with pytest.raises(S.SageError, match="sage workspace has not been prepared") as e:

@@ -129,6 +129,12 @@ def test_plan_range_checks(S):
         S.Plan.new(S.Shape(1, 1, 2**64 - 1))
     with pytest.raises(S.SageError, match="batch .* heads"):
         S.Plan.new(S.Shape(2**40, 2**30, 128))
+    # A frame layout whose token count wraps 64 bits is refused: 2 frames of
+    # 2^63 + 1 tokens would otherwise wrap to the sequence's 2 tokens.
+    with pytest.raises(S.SageError, match="covers more than 2\\^64 tokens, the sequence has 2"):
+        S.Plan.new(S.Shape(1, 1, 2), S.KvMerge.Pool(2, S.FrameLayout(2, 1, 1, 2**63, 0)))
+    with pytest.raises(S.SageError, match="covers more than 2\\^64 tokens"):
+        S.Plan.new(S.Shape(1, 1, 2), S.KvMerge.Pool(2, S.FrameLayout(1, 0, 2**32, 2**32, 0)))
     # The largest sizes that fit are accepted.
     p = S.Plan.new(S.Shape(1, 1, 2**31 - 128))
     assert p.tq_pad == 2**31 - 128 and p.tk_pad == 2**31 - 128
