@@ -438,23 +438,28 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
         const float* vmean = stats + bhk * 4 * D + D;
         const float* vscale = vmean + D;
         uint16_t* orow = out + b * g.o_sb + (long long)qi * g.o_st + h * g.o_sh;
-        const bool f16 = g.flags & F_OUT_F16;
+        // Pairs of outputs go through gfx950's packed converters
+        // (v_cvt_pk_bf16_f32, v_cvt_pk_f16_f32: round to nearest even), one
+        // uniform branch on the output type.
+        auto emit = [&](auto pack) __attribute__((always_inline)) {
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++)
+            for (int dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int d0 = 32 * dt + 8 * j + 4 * half;
-                uint32_t bits[4];
+                for (int j = 0; j < 4; j++) {
+                    const int d0 = 32 * dt + 8 * j + 4 * half;
+                    float y[4];
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float y = fmaf(o[dt][4 * j + r] * inv, vscale[d0 + r], vmean[d0 + r]);
-                    bits[r] = f16 ? f16_bits(y) : bf16_bits(y);
+                    for (int r = 0; r < 4; r++) y[r] = fmaf(o[dt][4 * j + r] * inv, vscale[d0 + r], vmean[d0 + r]);
+                    uint2 w;
+                    w.x = pack(y[0], y[1]);
+                    w.y = pack(y[2], y[3]);
+                    *reinterpret_cast<uint2*>(orow + d0) = w;
                 }
-                uint2 w;
-                w.x = bits[0] | (bits[1] << 16);
-                w.y = bits[2] | (bits[3] << 16);
-                *reinterpret_cast<uint2*>(orow + d0) = w;
-            }
+        };
+        if (g.flags & F_OUT_F16)
+            emit([](float a, float b) { return pack_f16x2(a, b); });
+        else
+            emit([](float a, float b) { return pack_bf16x2(a, b); });
     }
 }
 

@@ -125,15 +125,17 @@ __device__ __forceinline__ uint32_t e4m3_pair(float a, float b) {
     return r;
 }
 
-// f32 -> bf16 bits, round to nearest even, NaN kept (reference.rs:13-20).
-__device__ __forceinline__ uint32_t bf16_bits(float x) {
-    const uint32_t u = __float_as_uint(x);
-    if (x != x) return (u >> 16) | 0x40u;
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+// Two f32 -> one register of two bf16 / fp16 (low half first), rounded to
+// nearest even like the reference's f32 -> bf16 conversion
+// (reference.rs:13-20); a NaN stays a NaN.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
-
-__device__ __forceinline__ uint32_t f16_bits(float x) {
-    return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)x);
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
 }
 
 // Byte position of key k (0..63) of a 64-key block inside each channel row of
