@@ -39,7 +39,8 @@
 //   its SIMD fill the MFMA and VALU gaps: three a SIMD at head dim 128 (its
 //   Q^T operands wait in LDS to make room), four at head dim 64.
 // - Workgroups are dealt to XCDs so that the ones sharing a head's K and V
-//   share an L2.
+//   share an L2; causal tiles are dealt longest first across each XCD's
+//   heads.
 // - KV merging (MERGE, the reference's sg_attn_merge, sage_attn.cu:238-246,
 //   264-305): every key carries a log2(member count) bias, staged per block
 //   in LDS beside K and V. The log2 logit x = S * sc + bias is formed before
@@ -96,6 +97,15 @@ __device__ __forceinline__ int xcd_tile(int lin, int total) {
     return (lin % NUM_XCD) * per + lin / NUM_XCD;
 }
 
+// A causal query tile qt sweeps 2 qt + 2 key blocks. Dealt head by head,
+// the heavy tiles of an XCD's last head start late and finish alone; dealt
+// longest first across the XCD's heads, the short tiles fill the tail. That
+// order needs every XCD to hold whole heads (the plain mapping above does
+// then too, so the L2 sharing is unchanged).
+__device__ __forceinline__ bool causal_longest_first(int total, int ntq) {
+    return total % NUM_XCD == 0 && (total / NUM_XCD) % ntq == 0;
+}
+
 __device__ __forceinline__ bool half_selector(int lane) {
     return (int)__builtin_amdgcn_permlane32_swap(lane, lane, false, false)[0] != lane;
 }
@@ -135,9 +145,21 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 31, half = lane >> 5;
     const int ntq = gridDim.x;
-    const int tile = xcd_tile(blockIdx.x + ntq * (blockIdx.y + gridDim.y * blockIdx.z), ntq * gridDim.y * gridDim.z);
-    const int qt = CAUSAL ? ntq - 1 - tile % ntq : tile % ntq;  // causal: heavy tiles first
-    const int h = (tile / ntq) % g.heads, b = tile / (ntq * g.heads), hk = h / g.group;
+    const int lin = blockIdx.x + ntq * (blockIdx.y + gridDim.y * blockIdx.z), total = ntq * gridDim.y * gridDim.z;
+    int qt, hb;  // query tile; head slot b * heads + h
+    if (CAUSAL && causal_longest_first(total, ntq)) {
+        // XCD x holds head slots [x * hx, (x + 1) * hx); its i-th workgroup
+        // takes query tile ntq - 1 - i / hx of head slot x * hx + i % hx, so
+        // the XCD deals its tiles longest first across all of its heads.
+        const int per = total / NUM_XCD, hx = per / ntq, x = lin % NUM_XCD, i = lin / NUM_XCD;
+        qt = ntq - 1 - i / hx;
+        hb = x * hx + i % hx;
+    } else {
+        const int tile = xcd_tile(lin, total);
+        qt = CAUSAL ? ntq - 1 - tile % ntq : tile % ntq;  // causal: heavy tiles of a head first
+        hb = tile / ntq;
+    }
+    const int h = hb % g.heads, b = hb / g.heads, hk = h / g.group;
     const long long bh = (long long)b * g.heads + h, bhk = (long long)b * g.kv_heads + hk;
     const int q0 = qt * ATTN_ROWS + wave * 32;  // first query of this wave
     const int qi = q0 + col;                    // this lane's query
