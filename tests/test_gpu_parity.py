@@ -39,12 +39,16 @@ def _case(oracle, name):
         "tokens_x10": (P(1, 3, 700, 64, dtype=1), G(k_off_std=3.0, token_frac=0.02, token_scale=10.0, seed=10)),
         "outlier_ch20": (P(1, 2, 1000, 128, dtype=1, causal=True),
                          G(k_off_std=2.0, outlier_channels=4, outlier_scale=20.0, seed=12)),
+        # Causal with batch x heads a multiple of the 8 XCDs: the kernel deals the
+        # tiles longest first across each XCD's head slots (2 and 1 slots per XCD).
+        "d128_causal_b2_xcd": (P(2, 8, 700, 128, kv_heads=4, causal=True), G(k_off_std=2.0, seed=13)),
+        "d64_causal_b2_xcd": (P(2, 4, 260, 64, dtype=1, causal=True), G(k_off_std=2.0, seed=14)),
     }
     return cases[name]
 
 
 SMALL = ["c1", "d128_tail200", "d64_t3001", "d128_gqa", "d64_nosmooth", "d128_causal_f16", "d64_causal_gqa",
-         "n1", "n65", "tokens_x10", "outlier_ch20"]
+         "n1", "n65", "tokens_x10", "outlier_ch20", "d128_causal_b2_xcd", "d64_causal_b2_xcd"]
 
 
 def _check_attention(oracle, p, pro_oracle, o_gpu, rows, q, k, v, label):
