@@ -36,8 +36,9 @@
 //   256-byte lines (conflict-free b128 operand reads), filled by direct
 //   global -> LDS loads from a uniform SGPR base (no staging registers).
 // - A wave runs one block at a time (QK^T, softmax, P.V); the other waves on
-//   its SIMD fill the MFMA and VALU gaps: three a SIMD at head dim 128 (its
-//   Q^T operands wait in LDS to make room), four at head dim 64.
+//   its SIMD fill the MFMA and VALU gaps: three a SIMD at head dim 128, four
+//   at head dim 64. Q^T stays in registers; at head dim 128 the K operands
+//   of one 32-key sub-tile at a time make room for it.
 // - Workgroups are dealt to XCDs so that the ones sharing a head's K and V
 //   share an L2; causal tiles are dealt longest first across each XCD's
 //   heads.
@@ -106,6 +107,13 @@ __device__ __forceinline__ bool causal_longest_first(int total, int ntq) {
     return total % NUM_XCD == 0 && (total / NUM_XCD) % ntq == 0;
 }
 
+// This lane's index in the wave, rebuilt from v_mbcnt: values derived from the
+// lane are recomputed where a rare path or the epilogue needs them instead of
+// being kept live (or spilled) across the key loop.
+__device__ __forceinline__ int lane_now() {
+    return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
 __device__ __forceinline__ bool half_selector(int lane) {
     return (int)__builtin_amdgcn_permlane32_swap(lane, lane, false, false)[0] != lane;
 }
@@ -119,9 +127,6 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
                                                     const float* __restrict__ kbias, uint16_t* __restrict__ out,
                                                     Geom g) {
     constexpr int BN = ATTN_BN;
-    // Head dim 128 keeps its Q^T operands in LDS (three waves a SIMD fit in
-    // the registers then); head dim 64 keeps them in registers (four waves).
-    constexpr bool Q_IN_LDS = D == 128;
     constexpr int KS = D / 32;            // INT8 k-steps of 32 channels
     constexpr int DT = D / 32;            // 32-channel tiles of O^T
     constexpr int TILE = BN * D;          // bytes of one K tile and of one V tile
@@ -137,8 +142,6 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
     __shared__ __attribute__((aligned(16))) uint8_t ldsK1[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t ldsV0[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t ldsV1[TILE];
-    // Q^T operands, [wave][k-step][lane] (head dim 128 only).
-    __shared__ v4i ldsQ[Q_IN_LDS ? 4 : 1][KS][64];
     // Merge biases of the current and the next block.
     __shared__ __attribute__((aligned(16))) float ldsB0[MERGE ? BN : 4];
     __shared__ __attribute__((aligned(16))) float ldsB1[MERGE ? BN : 4];
@@ -176,13 +179,8 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
     // Consume the Q loads here, before the first barrier: otherwise the
     // compiler sinks them into the key loop and waits for every outstanding
     // load there, prefetches included.
-    if constexpr (Q_IN_LDS) {
 #pragma unroll
-        for (int s = 0; s < KS; s++) ldsQ[wave][s][lane] = qa[s];
-    } else {
-#pragma unroll
-        for (int s = 0; s < KS; s++) asm volatile("" ::"v"(qa[s]));
-    }
+    for (int s = 0; s < KS; s++) asm volatile("" ::"v"(qa[s]));
     asm volatile("" ::"v"(qs));
 
     int nblk = g.kblocks;
@@ -246,21 +244,37 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
     for (int r = 0; r < 16; r++) magic[r] = MAGIC_BITS;
     opaque_vgpr(magic);  // kept in VGPRs, not rebuilt before every block
     auto qk = [&](const uint8_t* kt, v16i (&s)[2]) __attribute__((always_inline)) {
-        v4i qb[KS];
+        const v4i (&qb)[KS] = qa;
+        if constexpr (D == 128) {
+            // One 32-key sub-tile's K operands at a time: the registers this
+            // saves hold the Q^T operands.
 #pragma unroll
-        for (int ks = 0; ks < KS; ks++) qb[ks] = Q_IN_LDS ? ldsQ[wave][ks][lane] : qa[ks];
-        uint4 ka[2][KS];
+            for (int t = 0; t < 2; t++) {
+                uint4 ka[KS];
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+                for (int ks = 0; ks < KS; ks++)
+                    ka[ks] = *reinterpret_cast<const uint4*>(kt + 16 * 32 * t * KCPR + koff[ks]);
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++)
-                ka[t][ks] = *reinterpret_cast<const uint4*>(kt + 16 * 32 * t * KCPR + koff[ks]);
+                for (int ks = 0; ks < KS; ks++) {
+                    const v4i av = {(int)ka[ks].x, (int)ka[ks].y, (int)ka[ks].z, (int)ka[ks].w};
+                    s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qb[ks], ks ? s[t] : magic, 0, 0, 0);
+                }
+                if (t == 0) __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            uint4 ka[2][KS];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
+            for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-                const v4i av = {(int)ka[t][ks].x, (int)ka[t][ks].y, (int)ka[t][ks].z, (int)ka[t][ks].w};
-                s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qb[ks], ks ? s[t] : magic, 0, 0, 0);
+                for (int ks = 0; ks < KS; ks++)
+                    ka[t][ks] = *reinterpret_cast<const uint4*>(kt + 16 * 32 * t * KCPR + koff[ks]);
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    const v4i av = {(int)ka[t][ks].x, (int)ka[t][ks].y, (int)ka[t][ks].z, (int)ka[t][ks].w};
+                    s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qb[ks], ks ? s[t] : magic, 0, 0, 0);
+                }
             }
         }
     };
@@ -335,8 +349,9 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
             // Keys past the sequence, and keys after the query when causal. Element
             // (t, r) is key blk*BN + 4*half + c with the constant c below, so one
             // per-lane limit decides every element.
-            int lim = g.tk - blk * BN - 4 * half;
-            if (CAUSAL) lim = min(lim, qi - blk * BN - 4 * half + 1);
+            const int ln = D == 128 ? lane_now() : lane, hf = ln >> 5;
+            int lim = g.tk - blk * BN - 4 * hf;
+            if (CAUSAL) lim = min(lim, q0 + (ln & 31) - blk * BN - 4 * hf + 1);
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
@@ -456,10 +471,11 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
     // out = O / l * v_scale + v_mean; lane holds channels 32dt + 8j + 4*half + 0..3.
     const float lt = l + swap_halves(l, sel);
     const float inv = 1.0f / lt;
-    if (qi < g.tokens) {
+    const int ln_e = D == 128 ? lane_now() : lane, half_e = ln_e >> 5, qi_e = q0 + (ln_e & 31);
+    if (qi_e < g.tokens) {
         const float* vmean = stats + bhk * 4 * D + D;
         const float* vscale = vmean + D;
-        uint16_t* orow = out + b * g.o_sb + (long long)qi * g.o_st + h * g.o_sh;
+        uint16_t* orow = out + b * g.o_sb + (long long)qi_e * g.o_st + h * g.o_sh;
         // Pairs of outputs go through gfx950's packed converters
         // (v_cvt_pk_bf16_f32, v_cvt_pk_f16_f32: round to nearest even), one
         // uniform branch on the output type.
@@ -468,7 +484,7 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const int d0 = 32 * dt + 8 * j + 4 * half;
+                    const int d0 = 32 * dt + 8 * j + 4 * half_e;
                     float y[4];
 #pragma unroll
                     for (int r = 0; r < 4; r++) y[r] = fmaf(o[dt][4 * j + r] * inv, vscale[d0 + r], vmean[d0 + r]);
