@@ -38,6 +38,18 @@ def test_gpu_attention_has_no_spill(torch_gpu):
         assert spill == 0, f"the attention kernel spills at head dim {d}"
 
 
+def test_gpu_attention_keeps_its_occupancy(torch_gpu):
+    """This build's occupancy (no reference counterpart): a SIMD holds 512
+    VGPRs a lane, so head dim 128 must stay within 168 (three waves a SIMD) and
+    head dim 64 within 128 (four waves). A change that crosses either limit
+    loses a wave per SIMD without failing any numerical test."""
+    import spl_sage as S
+
+    for d, limit in ((64, 128), (128, 168)):
+        regs, _ = S.SageAttention(None, d).attn_resources()
+        assert regs <= limit, f"head dim {d}: {regs} VGPRs > {limit}"
+
+
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("smooth", [True, False])
 def test_gpu_attention_matches_float_reference(oracle, torch_gpu, d, smooth):
