@@ -58,9 +58,12 @@ typedef enum sage_dtype { SAGE_BF16 = 0, SAGE_F16 = 1 } sage_dtype;
  * stay fp32 under both settings (at least as accurate as f16 partials). */
 typedef enum sage_pv_accum { SAGE_PV_F32 = 0, SAGE_PV_F16 = 1 } sage_pv_accum;
 
-/* Tile (mod.rs:116-168), re-read for CDNA4: `warps` = wave64s per workgroup,
- * `m_tiles` = 32-query MFMA column tiles per wave, `stages` = K/V LDS
- * buffers. Rows per workgroup = 32 * m_tiles * warps. */
+/* Tile (mod.rs:116-168): the reference's CTA shape (warps, 16-row m-tiles per
+ * warp, K/V ring stages; 16 * m_tiles * warps rows a CTA). Accepted exactly
+ * as Tile::validate accepts it; it tunes the reference's NVIDIA kernel, and
+ * every accepted tile runs here on the one CDNA4 configuration (4 wave64s of
+ * 32 queries, 128 queries a workgroup, double-buffered K/V), so results do not
+ * depend on it. */
 typedef struct sage_tile {
     uint32_t warps;
     uint32_t m_tiles;
@@ -194,10 +197,13 @@ sage_status sage_strides_check(const sage_strides* s, const char* what);
 uint64_t sage_strides_extent(const sage_strides* s, uint64_t batch, uint64_t tokens, uint64_t heads,
                              uint64_t head_dim);
 
-/* Tile::validate (mod.rs:158-167) for this build's tile menu. */
+/* Tile::validate (mod.rs:158-167): warps in {2,4,8}, m_tiles in {1,2,4},
+ * stages 2..6, 128 a multiple of 16 * m_tiles * warps; otherwise
+ * "unsupported sage tile Tile { .. }". */
 sage_status sage_tile_validate(const sage_tile* t);
 
-/* Config::for_head_dim (mod.rs:194-200). */
+/* Config::for_head_dim (mod.rs:194-200): Tile::D128 {4,1,3} above head dim
+ * 64, Tile::DEFAULT {4,2,3} otherwise (mod.rs:128-147); PvAccum::F32. */
 sage_config sage_config_for_head_dim(uint64_t head_dim);
 
 /* check_device (mod.rs:552-566): fails unless device `ordinal` is gfx950. */
@@ -215,6 +221,17 @@ void* sage_stream(const sage_attention* s);                  /* mod.rs:636-638 *
 /* attn_resources (mod.rs:640-646): VGPRs per lane and scratch (spill) bytes
  * of the attention kernel, plus its static LDS bytes. */
 sage_status sage_attn_resources(const sage_attention* s, int32_t* regs, int32_t* spill, int32_t* lds);
+
+/* The same for each attention kernel the context can launch (extension: the
+ * reference reports its dense kernel only): SAGE_KERNEL_DENSE, _CAUSAL (the
+ * causal extension) or _MERGED (KV merging, sg_attn_merge). */
+typedef enum sage_attn_kernel {
+    SAGE_KERNEL_DENSE = 0,
+    SAGE_KERNEL_CAUSAL = 1,
+    SAGE_KERNEL_MERGED = 2
+} sage_attn_kernel;
+sage_status sage_attn_kernel_resources(const sage_attention* s, int32_t kernel, int32_t* regs, int32_t* spill,
+                                       int32_t* lds);
 
 /* SageAttention::workspace (mod.rs:648-670): allocates (and zero-fills) the
  * buffers for `shape` and `merge`. A shape whose buffers would need more than

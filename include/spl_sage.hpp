@@ -51,13 +51,17 @@ enum class Dtype : int32_t { Bf16 = SAGE_BF16, F16 = SAGE_F16 };
 // PvAccum (mod.rs:170-181).
 enum class PvAccum : int32_t { F32 = SAGE_PV_F32, F16 = SAGE_PV_F16 };
 
-// Tile (mod.rs:116-168): wave64s per workgroup, 32-query MFMA tiles per
-// wave, K/V LDS buffers.
+// Tile (mod.rs:116-168): the reference's CTA shape (warps, 16-row m-tiles,
+// K/V ring stages). Validated as the reference validates it; every valid
+// tile runs on the library's one CDNA4 configuration, so it does not change
+// results.
 struct Tile {
-    uint32_t warps = 4, m_tiles = 1, stages = 2;
+    uint32_t warps = 4, m_tiles = 2, stages = 3;
 
+    static const Tile DEFAULT;  // mod.rs:128-132
+    static const Tile D128;     // mod.rs:136-140
     static Tile for_head_dim(std::size_t head_dim);
-    std::size_t rows() const { return 32u * m_tiles * warps; }
+    std::size_t rows() const { return 16u * m_tiles * warps; }
     sage_tile raw() const { return sage_tile{warps, m_tiles, stages}; }
     void validate() const {
         const sage_tile t = raw();
@@ -77,6 +81,8 @@ struct Config {
     sage_config raw() const { return sage_config{tile.raw(), static_cast<int32_t>(pv_accum)}; }
 };
 
+inline const Tile Tile::DEFAULT{4, 2, 3};
+inline const Tile Tile::D128{4, 1, 3};
 inline Tile Tile::for_head_dim(std::size_t head_dim) { return Config::for_head_dim(head_dim).tile; }
 
 // Shape (mod.rs:262-268); kv_heads (0 = heads) is the grouped-query extension.

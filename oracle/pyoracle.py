@@ -48,6 +48,26 @@ class _GenSpec(C.Structure):
     ]
 
 
+class _Numerics(C.Structure):
+    _fields_ = [("l_from_p8", C.c_int), ("pow2_max", C.c_int), ("tau", C.c_float), ("exp_f16", C.c_int)]
+
+
+@dataclass(frozen=True)
+class Numerics:
+    """Alternative softmax numerics (all defaults = the reference's): l from
+    the E4M3-rounded P; the running max rounded up to an integer in log2
+    units (power-of-two rescales); headroom tau before the max moves; p
+    rounded to f16."""
+
+    l_from_p8: bool = False
+    pow2_max: bool = False
+    tau: float = 0.0
+    exp_f16: bool = False
+
+    def _c(self) -> _Numerics:
+        return _Numerics(int(self.l_from_p8), int(self.pow2_max), float(self.tau), int(self.exp_f16))
+
+
 _lib = None
 
 
@@ -101,6 +121,11 @@ def lib() -> C.CDLL:
         l.oracle_attention_f64.argtypes = [C.POINTER(_Problem), C.c_int, C.c_float, vp, vp, vp, vp, C.c_int, vp, C.c_int]
         l.oracle_sage_emulate.argtypes = [C.POINTER(_Problem), C.c_int, vp, vp, vp, vp, vp, vp, vp, vp, C.c_int, vp,
                                           vp, C.c_int, C.c_int, C.c_int]
+        l.oracle_sage_emulate_numerics.argtypes = [C.POINTER(_Problem), C.c_int, vp, vp, vp, vp, vp, vp, vp, vp,
+                                                   C.c_int, C.c_int, vp, vp, C.c_int, C.c_int,
+                                                   C.POINTER(_Numerics), C.c_int]
+        l.oracle_attention_f64_rows.argtypes = [C.POINTER(_Problem), C.c_int, C.c_float, vp, vp, vp, vp, C.c_int,
+                                                C.c_int, vp, C.c_int]
         l.oracle_errors.argtypes = [vp, vp, C.c_size_t, vp]
         _lib = l
     return _lib
@@ -283,36 +308,45 @@ def prologue(p: Problem, q: np.ndarray, k: np.ndarray, v: np.ndarray, threads: i
     return out
 
 
-def _rows(rows, n):
+def _rows(rows, p: Problem):
+    """rows: None (all), a 1-D array shared by every (b, h), or a
+    [B*H, R] array of per-(b, h) rows. Returns (array or None, R, stride)."""
     if rows is None:
-        return None, n
+        return None, p.tokens, 0
     r = np.ascontiguousarray(rows, dtype=np.int32)
-    assert r.min() >= 0 and r.max() < n
-    return r, len(r)
+    assert r.min() >= 0 and r.max() < p.tokens
+    if r.ndim == 2:
+        assert r.shape[0] == p.batch * p.heads
+        return r, r.shape[1], r.shape[1]
+    return r, len(r), 0
 
 
 def attention_f64(p: Problem, q, k, v, rows=None, threads: int = 0) -> np.ndarray:
     """f64 softmax attention (reference.rs:148-184), [B, H, R, D] float32."""
-    r, R = _rows(rows, p.tokens)
+    r, R, rs = _rows(rows, p)
     out = np.empty((p.batch, p.heads, R, p.head_dim), np.float32)
     q, k, v = (np.ascontiguousarray(a, dtype=np.uint16) for a in (q, k, v))
-    lib().oracle_attention_f64(C.byref(p._c()), int(p.causal), float(p.scale()), _p(q), _p(k), _p(v),
-                               None if r is None else _p(r), R, _p(out), threads)
+    lib().oracle_attention_f64_rows(C.byref(p._c()), int(p.causal), float(p.scale()), _p(q), _p(k), _p(v),
+                                    None if r is None else _p(r), R, rs, _p(out), threads)
     return out
 
 
-def sage_emulate(p: Problem, pro: dict, rows=None, out_dtype: int = BF16, threads: int = 0, fast_exp: bool = True):
+def sage_emulate(p: Problem, pro: dict, rows=None, out_dtype: int = BF16, threads: int = 0, fast_exp: bool = True,
+                 numerics: Numerics | None = None):
     """The reference's quantised attention arithmetic on `pro`; returns
     (float32 [B,H,R,D] before 16-bit rounding, uint16 codes of out_dtype).
     fast_exp=True is the reference's default logit arithmetic (SG_FAST_EXP=1,
-    sage_attn.cu:59-61); False converts the scores exactly (SG_FAST_EXP=0)."""
-    r, R = _rows(rows, p.tokens)
+    sage_attn.cu:59-61); False converts the scores exactly (SG_FAST_EXP=0).
+    `numerics` selects an alternative softmax (None = the reference's)."""
+    r, R, rs = _rows(rows, p)
     out = np.empty((p.batch, p.heads, R, p.head_dim), np.float32)
     o16 = np.empty(out.shape, np.uint16)
     kb = np.ascontiguousarray(pro.get("kbias", np.zeros(p.tk_pad, np.float32)), dtype=np.float32)
-    lib().oracle_sage_emulate(C.byref(p._c()), int(p.causal), _p(pro["q8"]), _p(pro["q_scale"]), _p(pro["k8"]),
-                              _p(pro["k_scale"]), _p(pro["v8"]), _p(pro["stats"]), _p(kb),
-                              None if r is None else _p(r), R, _p(out), _p(o16), out_dtype, int(bool(fast_exp)), threads)
+    nv = None if numerics is None else C.byref(numerics._c())
+    lib().oracle_sage_emulate_numerics(C.byref(p._c()), int(p.causal), _p(pro["q8"]), _p(pro["q_scale"]),
+                                       _p(pro["k8"]), _p(pro["k_scale"]), _p(pro["v8"]), _p(pro["stats"]), _p(kb),
+                                       None if r is None else _p(r), R, rs, _p(out), _p(o16), out_dtype,
+                                       int(bool(fast_exp)), nv, threads)
     return out, o16
 
 

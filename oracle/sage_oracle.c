@@ -593,8 +593,9 @@ int oracle_prologue(const oracle_problem* p, const uint16_t* q, const uint16_t* 
  * Pinned: closed forms in tests (uniform keys give the mean of V; one-hot
  * logits select one V row; V = const gives const), numpy/torch float64, and
  * the reference's merged == dense identity on uniform cells (tests.rs:193-232). */
-void oracle_attention_f64(const oracle_problem* p, int causal, float scale, const uint16_t* q, const uint16_t* k,
-                          const uint16_t* v, const int* rows, int nrows, float* out, int threads) {
+void oracle_attention_f64_rows(const oracle_problem* p, int causal, float scale, const uint16_t* q,
+                               const uint16_t* k, const uint16_t* v, const int* rows, int nrows, int rows_stride,
+                               float* out, int threads) {
     const int B = p->batch, H = p->heads, HK = p->kv_heads, N = p->tokens, D = p->head_dim, G = H / HK;
     const int TK = oracle_merged_keys(p);
     const int R = rows ? nrows : N;
@@ -638,7 +639,7 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
         for (int bh = 0; bh < B * H; bh++)
             for (int ri = 0; ri < R; ri++) {
                 int b = bh / H, h = bh % H, hk = h / G;
-                int i = rows ? rows[ri] : ri;
+                int i = rows ? rows[(size_t)bh * rows_stride + ri] : ri;
                 read_row(p, q, p->q_sb, p->q_st, p->q_sh, b, h, i, qf);
                 if (p->ln) oracle_layernorm_f64(qf, qf, D, p->ln, p->ln + D, p->ln_eps);
                 for (int d = 0; d < D; d++) qi[d] = qf[d];
@@ -673,6 +674,11 @@ void oracle_attention_f64(const oracle_problem* p, int causal, float scale, cons
     free(kb);
 }
 
+void oracle_attention_f64(const oracle_problem* p, int causal, float scale, const uint16_t* q, const uint16_t* k,
+                          const uint16_t* v, const int* rows, int nrows, float* out, int threads) {
+    oracle_attention_f64_rows(p, causal, scale, q, k, v, rows, nrows, 0, out, threads);
+}
+
 /* Correctly rounded exp2 in f32 (the build's stand-in for a hardware exp2;
  * the reference's ex2.approx is an NVIDIA approximation and is not restated). */
 static inline float ex2f_cr(float x) { return (float)exp2((double)x); }
@@ -696,11 +702,29 @@ static inline float ex2f_cr(float x) { return (float)exp2((double)x); }
  * Masked keys (padding, and j > i when causal) have p = 0.
  * Pinned: closed forms in tests (uniform Q gives the V-code mean; a block of
  * equal scores gives equal weights) and agreement with oracle_attention_f64
- * within the quantisation error; sequential sums replace the GPU's lane order. */
-void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, const float* q_scale,
-                         const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* stats,
-                         const float* kbias, const int* rows, int nrows, float* out, uint16_t* out16, int out_dtype,
-                         int fast_exp, int threads) {
+ * within the quantisation error; sequential sums replace the GPU's lane order.
+ *
+ * `nv` (NULL = the reference's numerics above) selects alternative softmax
+ * numerics, for judging them against the reference's on the CPU:
+ *   l_from_p8: l sums the E4M3-rounded P, so the weights of the output and of
+ *     its normaliser round together;
+ *   pow2_max:  the running max m moves to ceil(block max) (log2 units), so
+ *     alpha = 2^(m_old - m_new) is a power of two and the row's largest P
+ *     lies in (224, 448];
+ *   tau:       m moves only when a block's max exceeds it, to that max plus
+ *     tau (pow2_max: ceil of the max, plus tau); P = 448 * 2^(x - m) keeps
+ *     every P at or below 448; tau = 0 with pow2_max = 0 is the reference;
+ *   exp_f16:   every p (and alpha) is rounded to the nearest f16 value.
+ * `rows_stride` > 0 gives every (b, h) its own rows: rows + bh * rows_stride.
+ * Pinned (tests/test_oracle_numerics.py): per-(b, h) rows select what shared
+ * rows select; default numerics equal the reference's bit for bit; a query
+ * seeing one key returns that value when l sums the E4M3 P; a query seeing two
+ * keys matches the float64 closed form of every mode. */
+void oracle_sage_emulate_numerics(const oracle_problem* p, int causal, const int8_t* q8, const float* q_scale,
+                                  const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* stats,
+                                  const float* kbias, const int* rows, int nrows, int rows_stride, float* out,
+                                  uint16_t* out16, int out_dtype, int fast_exp, const oracle_numerics* nv,
+                                  int threads) {
     const int B = p->batch, H = p->heads, HK = p->kv_heads, N = p->tokens, D = p->head_dim, G = H / HK;
     const float kMagic = 12582912.0f; /* 1.5 * 2^23 */
     const int TK = oracle_merged_keys(p), merged = merging(p);
@@ -708,6 +732,8 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
     const int nblk = (int)(tk_pad / ORACLE_KBLOCK);
     const int R = rows ? nrows : N;
     const float kLog448 = 8.807354922057604f;
+    const oracle_numerics ref_nv = {0, 0, 0.f, 0};
+    const oracle_numerics nm = nv ? *nv : ref_nv;
     float v8f[256];
     for (int c = 0; c < 256; c++) v8f[c] = oracle_e4m3_to_f32((uint8_t)c);
     set_threads(threads);
@@ -721,7 +747,7 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
         for (int bh = 0; bh < B * H; bh++)
             for (int ri = 0; ri < R; ri++) {
                 const int b = bh / H, h = bh % H, hk = h / G, bhk = b * HK + hk;
-                const int i = rows ? rows[ri] : ri;
+                const int i = rows ? rows[(size_t)bh * rows_stride + ri] : ri;
                 const int8_t* qi = q8 + ((size_t)bh * tq_pad + i) * D;
                 const float qs = q_scale[(size_t)bh * (tq_pad / ORACLE_QGROUP) + i / ORACLE_QGROUP];
                 const int8_t* kb = k8 + (size_t)bhk * tk_pad * D;
@@ -748,25 +774,28 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
                     /* x as the reference holds it: exact, or biased by kMagic (both exact floats) */
                     const float bias = fast_exp ? kMagic : 0.f;
                     const float xoff = fast_exp ? -kMagic * sc : 0.f;
-                    float mnew = m, off;
+                    float mnew = m, off, bmax = -INFINITY;
                     float X[ORACLE_KBLOCK];
                     if (merged) {
                         /* the log2 logit with the log-count bias; padding keys carry -inf */
-                        float mx = -INFINITY;
                         for (int r = 0; r < ORACLE_KBLOCK; r++) {
                             const int j = blk * ORACLE_KBLOCK + r;
                             const float kb = kbias[j];
                             const float bo = fast_exp ? fmaf(-kMagic, sc, kb) : kb;
                             X[r] = S[r] == INT32_MIN ? -INFINITY : fmaf(bias + (float)S[r], sc, bo);
-                            mx = fmaxf(mx, X[r]);
+                            bmax = fmaxf(bmax, X[r]);
                         }
-                        mnew = fmaxf(m, mx);
-                        off = kLog448 - mnew;
-                    } else {
-                        if (have) mnew = fmaxf(m, fmaf(bias + (float)smax, sc, xoff));
-                        off = (kLog448 - mnew) + xoff;
+                    } else if (have) {
+                        bmax = fmaf(bias + (float)smax, sc, xoff);
                     }
-                    const float alpha = ex2f_cr(m - mnew);
+                    if (nm.pow2_max || nm.tau != 0.f) {
+                        if (bmax > m) mnew = (nm.pow2_max ? ceilf(bmax) : bmax) + nm.tau;
+                    } else {
+                        mnew = fmaxf(m, bmax);
+                    }
+                    off = merged ? kLog448 - mnew : (kLog448 - mnew) + xoff;
+                    float alpha = ex2f_cr(m - mnew);
+                    if (nm.exp_f16) alpha = (float)oracle_round_f16(alpha);
                     m = mnew;
                     float sum = 0.f;
                     for (int r = 0; r < ORACLE_KBLOCK; r++) {
@@ -774,8 +803,9 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
                         if (S[r] == INT32_MIN) pr = 0.f;
                         else if (merged) pr = ex2f_cr(X[r] + off);
                         else pr = ex2f_cr(fmaf(bias + (float)S[r], sc, off));
+                        if (nm.exp_f16) pr = (float)oracle_round_f16(pr);
                         P[r] = pr;
-                        sum += pr;
+                        sum += nm.l_from_p8 ? v8f[oracle_f32_to_e4m3(pr)] : pr;
                     }
                     l = fmaf(l, alpha, sum);
                     for (int d = 0; d < D; d++) pv[d] = 0;
@@ -803,6 +833,14 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
         free(O);
         free(pv);
     }
+}
+
+void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, const float* q_scale,
+                         const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* stats,
+                         const float* kbias, const int* rows, int nrows, float* out, uint16_t* out16, int out_dtype,
+                         int fast_exp, int threads) {
+    oracle_sage_emulate_numerics(p, causal, q8, q_scale, k8, k_scale, v8, stats, kbias, rows, nrows, 0, out, out16,
+                                 out_dtype, fast_exp, NULL, threads);
 }
 
 /* reference.rs:202-225 */

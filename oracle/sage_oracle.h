@@ -185,6 +185,31 @@ void oracle_sage_emulate(const oracle_problem* p, int causal, const int8_t* q8, 
                          const float* kbias, const int* rows, int nrows, float* out, uint16_t* out16,
                          int out_dtype, int fast_exp, int threads);
 
+/* Alternative softmax numerics for oracle_sage_emulate_numerics (each 0 = the
+ * reference's): l from the E4M3-rounded P; the running max rounded up to an
+ * integer in log2 units (power-of-two rescales); headroom tau above the
+ * running max before it moves; p rounded to f16. */
+typedef struct {
+    int l_from_p8;
+    int pow2_max;
+    float tau;
+    int exp_f16;
+} oracle_numerics;
+
+/* oracle_sage_emulate with per-(b, h) rows (rows_stride > 0: the rows of bh
+ * start at rows + bh * rows_stride; 0: shared) and optional alternative
+ * numerics (nv == NULL: the reference's). */
+void oracle_sage_emulate_numerics(const oracle_problem* p, int causal, const int8_t* q8, const float* q_scale,
+                                  const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* stats,
+                                  const float* kbias, const int* rows, int nrows, int rows_stride, float* out,
+                                  uint16_t* out16, int out_dtype, int fast_exp, const oracle_numerics* nv,
+                                  int threads);
+
+/* oracle_attention_f64 with per-(b, h) rows, as above. */
+void oracle_attention_f64_rows(const oracle_problem* p, int causal, float scale, const uint16_t* q,
+                               const uint16_t* k, const uint16_t* v, const int* rows, int nrows, int rows_stride,
+                               float* out, int threads);
+
 /* Errors of `ours` against `ref` (reference.rs:202-225):
  * out[0] cos, [1] rel_l1, [2] rel_l2, [3] max_abs, [4] ref_max. */
 void oracle_errors(const float* ours, const float* ref, size_t n, double* out);

@@ -202,21 +202,29 @@ uint64_t sage_strides_extent(const sage_strides* s, uint64_t batch, uint64_t tok
     return e;
 }
 
-// This build's tile menu: 4 wave64s of one 32-query MFMA tile each, two K/V
-// LDS buffers (128 rows per workgroup).
+// Tile::validate (mod.rs:158-167): warps in {2, 4, 8}, m_tiles in {1, 2, 4},
+// stages 2..6, and the reference's rows per CTA (16 * m_tiles * warps)
+// dividing the 128-query tile. The tile tunes the reference's NVIDIA kernel;
+// every tile it accepts runs here on the one CDNA4 configuration (4 wave64s
+// of 32 queries, 128 queries a workgroup, double-buffered K/V), so outputs do
+// not depend on it.
 sage_status sage_tile_validate(const sage_tile* t) {
     if (!t) return fail(SAGE_ERR_INVALID, "null tile");
-    if (t->warps != 4 || t->m_tiles != 1 || t->stages != 2)
+    const bool warps_ok = t->warps == 2 || t->warps == 4 || t->warps == 8;
+    const bool mt_ok = t->m_tiles == 1 || t->m_tiles == 2 || t->m_tiles == 4;
+    const bool stages_ok = t->stages >= 2 && t->stages <= 6;
+    if (!warps_ok || !mt_ok || !stages_ok || SAGE_QTILE % (16u * t->m_tiles * t->warps) != 0)
         return fail(SAGE_ERR_INVALID, "unsupported sage tile %s", tile_dbg(*t).c_str());
     return ok();
 }
 
+// Config::for_head_dim (mod.rs:194-200) with Tile::for_head_dim (:128-147):
+// Tile::D128 {4, 1, 3} above head dim 64, Tile::DEFAULT {4, 2, 3} otherwise.
 sage_config sage_config_for_head_dim(uint64_t head_dim) {
-    (void)head_dim;
     sage_config c{};
     c.tile.warps = 4;
-    c.tile.m_tiles = 1;
-    c.tile.stages = 2;
+    c.tile.m_tiles = head_dim > 64 ? 1 : 2;
+    c.tile.stages = 3;
     c.pv_accum = SAGE_PV_F32;
     return c;
 }
@@ -267,9 +275,17 @@ sage_config sage_get_config(const sage_attention* s) { return s ? s->config : sa
 void* sage_stream(const sage_attention* s) { return s ? static_cast<void*>(s->stream) : nullptr; }
 
 sage_status sage_attn_resources(const sage_attention* s, int32_t* regs, int32_t* spill, int32_t* lds) {
+    return sage_attn_kernel_resources(s, SAGE_KERNEL_DENSE, regs, spill, lds);
+}
+
+sage_status sage_attn_kernel_resources(const sage_attention* s, int32_t kernel, int32_t* regs, int32_t* spill,
+                                       int32_t* lds) {
     if (!s || !regs || !spill || !lds) return fail(SAGE_ERR_INVALID, "null argument");
+    if (kernel != SAGE_KERNEL_DENSE && kernel != SAGE_KERNEL_CAUSAL && kernel != SAGE_KERNEL_MERGED)
+        return fail(SAGE_ERR_INVALID, "unknown attention kernel %d", kernel);
     int r = 0, sp = 0, l = 0;
-    hipError_t e = sage::attention_resources((int)s->head_dim, false, &r, &sp, &l);
+    hipError_t e = sage::attention_resources((int)s->head_dim, kernel == SAGE_KERNEL_CAUSAL,
+                                             kernel == SAGE_KERNEL_MERGED, &r, &sp, &l);
     if (e != hipSuccess) return hip_fail(e, "registers");
     *regs = r;
     *spill = sp;

@@ -520,15 +520,16 @@ hipError_t launch_attention(int head_dim, const AttendBufs& w, const Geom& g, hi
     return head_dim == 64 ? launch_dim<64>(w, g, s) : launch_dim<128>(w, g, s);
 }
 
-hipError_t attention_resources(int head_dim, bool causal, int* regs, int* spill, int* lds) {
+template <int D>
+static const void* attention_kernel(bool causal, bool merge) {
+    if (merge) return reinterpret_cast<const void*>(&sage_attn<D, false, true>);
+    return causal ? reinterpret_cast<const void*>(&sage_attn<D, true, false>)
+                  : reinterpret_cast<const void*>(&sage_attn<D, false, false>);
+}
+
+hipError_t attention_resources(int head_dim, bool causal, bool merge, int* regs, int* spill, int* lds) {
     hipFuncAttributes a;
-    const void* f;
-    if (head_dim == 64)
-        f = causal ? reinterpret_cast<const void*>(&sage_attn<64, true, false>)
-                   : reinterpret_cast<const void*>(&sage_attn<64, false, false>);
-    else
-        f = causal ? reinterpret_cast<const void*>(&sage_attn<128, true, false>)
-                   : reinterpret_cast<const void*>(&sage_attn<128, false, false>);
+    const void* f = head_dim == 64 ? attention_kernel<64>(causal, merge) : attention_kernel<128>(causal, merge);
     hipError_t e = hipFuncGetAttributes(&a, f);
     if (e != hipSuccess) return e;
     *regs = a.numRegs;

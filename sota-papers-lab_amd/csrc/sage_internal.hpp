@@ -42,8 +42,9 @@ constexpr int ATTN_ROWS = 128;
 
 hipError_t launch_attention(int head_dim, const AttendBufs& w, const Geom& g, hipStream_t s);
 
-// Kernel resources of the attention kernel for head_dim (VGPRs, scratch, LDS).
-hipError_t attention_resources(int head_dim, bool causal, int* regs, int* spill, int* lds);
+// Kernel resources (VGPRs, scratch, LDS) of the attention kernel for
+// head_dim: dense, causal or KV-merged.
+hipError_t attention_resources(int head_dim, bool causal, bool merge, int* regs, int* spill, int* lds);
 
 // MFMA peak probe: which 0 = INT8, 1 = FP8, 2 = BF16; returns dense TOPS.
 hipError_t run_peak(int which, int iters, hipStream_t s, double* tops);

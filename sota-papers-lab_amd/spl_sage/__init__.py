@@ -47,15 +47,17 @@ def _check(status: int) -> None:
 
 @dataclass(frozen=True)
 class Tile:
-    """mod.rs:116-168; on CDNA4 `warps` counts wave64s, `m_tiles` 32-query
-    MFMA tiles per wave, `stages` K/V LDS buffers."""
+    """mod.rs:116-168: the reference's CTA shape (warps, 16-row m-tiles,
+    K/V ring stages), validated as the reference validates it. Every valid
+    tile runs on the library's one CDNA4 configuration, so it does not change
+    results."""
 
     warps: int
     m_tiles: int
     stages: int
 
     def rows(self) -> int:
-        return 32 * self.m_tiles * self.warps
+        return 16 * self.m_tiles * self.warps
 
     def validate(self) -> None:
         _check(lib().sage_tile_validate(C.byref(self._c())))
@@ -68,8 +70,8 @@ class Tile:
         return Config.for_head_dim(head_dim).tile
 
 
-Tile.DEFAULT = Tile(4, 1, 2)
-Tile.D128 = Tile(4, 1, 2)
+Tile.DEFAULT = Tile(4, 2, 3)  # mod.rs:128-132
+Tile.D128 = Tile(4, 1, 3)  # mod.rs:136-140
 
 
 class PvAccum(enum.IntEnum):
@@ -455,6 +457,16 @@ class SageAttention:
         r, s, l = C.c_int32(), C.c_int32(), C.c_int32()
         _check(lib().sage_attn_resources(self._h, C.byref(r), C.byref(s), C.byref(l)))
         return r.value, s.value
+
+    KERNELS = {"dense": 0, "causal": 1, "merged": 2}
+
+    def attn_kernel_resources(self, kernel: str) -> tuple:
+        """(VGPRs per lane, scratch bytes per lane, static LDS bytes) of the
+        dense, causal or merged attention kernel (an extension)."""
+        r, s, l = C.c_int32(), C.c_int32(), C.c_int32()
+        _check(lib().sage_attn_kernel_resources(self._h, self.KERNELS[kernel], C.byref(r), C.byref(s),
+                                                C.byref(l)))
+        return r.value, s.value, l.value
 
     def workspace(self, shape: Shape, merge: KvMerge = KvMerge.Dense) -> Workspace:
         h = C.c_void_p()

@@ -97,6 +97,7 @@ SIGNATURES = {
     "sage_get_config": (sage_config, [C.c_void_p]),
     "sage_stream": (C.c_void_p, [C.c_void_p]),
     "sage_attn_resources": (i32, [C.c_void_p, P(i32), P(i32), P(i32)]),
+    "sage_attn_kernel_resources": (i32, [C.c_void_p, i32, P(i32), P(i32), P(i32)]),
     "sage_workspace_new": (i32, [C.c_void_p, P(sage_shape), P(sage_kv_merge), P(C.c_void_p)]),
     "sage_workspace_destroy": (None, [C.c_void_p]),
     "sage_workspace_bytes": (u64, [C.c_void_p]),

@@ -102,15 +102,30 @@ static void strides_cover_the_tensor() {
     Strides::bthd(5, 3, 64).check("x");
 }
 
-// mod.rs:116-201: this build's tile menu and the default config.
+// mod.rs:116-201: the reference's tile menu (Tile::validate) and its default
+// configs (Tile::DEFAULT, Tile::D128, Config::for_head_dim).
 static void tiles_and_config() {
-    for (std::size_t d : {64, 128}) {
-        const Config c = Config::for_head_dim(d);
-        CHECK(c.pv_accum == PvAccum::F32);
-        c.tile.validate();
-        CHECK(c.tile.rows() == 128);
-    }
-    EXPECT_ERROR((Tile{8, 1, 2}.validate()), SAGE_ERR_INVALID, "unsupported sage tile");
+    const Config c64 = Config::for_head_dim(64), c128 = Config::for_head_dim(128);
+    CHECK(c64.pv_accum == PvAccum::F32 && c128.pv_accum == PvAccum::F32);
+    CHECK(c64.tile.warps == 4 && c64.tile.m_tiles == 2 && c64.tile.stages == 3);
+    CHECK(c128.tile.warps == 4 && c128.tile.m_tiles == 1 && c128.tile.stages == 3);
+    CHECK(Tile::DEFAULT.rows() == 128 && Tile::D128.rows() == 64);
+    int accepted = 0;
+    for (uint32_t w = 0; w < 10; w++)
+        for (uint32_t m = 0; m < 6; m++)
+            for (uint32_t st = 0; st < 8; st++) {
+                const bool ref_ok = (w == 2 || w == 4 || w == 8) && (m == 1 || m == 2 || m == 4) && st >= 2 &&
+                                    st <= 6 && 128 % (16 * m * w) == 0;
+                if (ref_ok) {
+                    (Tile{w, m, st}).validate();
+                    accepted++;
+                } else {
+                    EXPECT_ERROR((Tile{w, m, st}.validate()), SAGE_ERR_INVALID, "unsupported sage tile");
+                }
+            }
+    CHECK(accepted == 30);
+    (Tile{8, 1, 2}).validate();
+    EXPECT_ERROR((Tile{4, 4, 3}.validate()), SAGE_ERR_INVALID, "unsupported sage tile");
 }
 
 // mod.rs:905-910 and the benchmark's operation counts.

@@ -17,15 +17,18 @@ def v8_logical(raw: np.ndarray, b: int, g: int, tk_pad: int, d: int) -> np.ndarr
     return np.ascontiguousarray(x.transpose(0, 1, 2, 4, 3)).reshape(b, g, tk_pad, d)
 
 
-def run(torch, p, q, k, v, out_dtype=None, q_layout="bthd", out_layout="bthd", want_ws=True):
+def run(torch, p, q, k, v, out_dtype=None, q_layout="bthd", out_layout="bthd", want_ws=True, tile=None):
     """Runs prepare + attend on the GPU. q, k, v are uint16 [B,T,H,D] codes.
-    Returns (dict of workspace buffers in logical layouts, uint16 output [B,T,H,D])."""
+    `tile` (an spl_sage.Tile, default Config::for_head_dim's) configures the
+    context. Returns (dict of workspace buffers in logical layouts, uint16
+    output [B,T,H,D])."""
     import spl_sage as S
 
     B, T, H, HK, D = p.batch, p.tokens, p.heads, p.hk, p.head_dim
     config = None
-    if p.pv16:
-        config = S.Config(S.Config.for_head_dim(D).tile, S.PvAccum.F16)
+    if p.pv16 or tile is not None:
+        config = S.Config(tile if tile is not None else S.Config.for_head_dim(D).tile,
+                          S.PvAccum.F16 if p.pv16 else S.PvAccum.F32)
     sa = S.SageAttention(None, D, config)
     merge = S.KvMerge.Dense
     if p.merge > 1:
@@ -102,6 +105,30 @@ def sample_rows(n: int, count: int, seed: int = 0) -> np.ndarray:
     return np.array(sorted(r), dtype=np.int32)
 
 
+def tile_rows(n: int, heads_total: int, per_tile: int = 1, seed: int = 0) -> np.ndarray:
+    """[heads_total, R] query rows: for every (batch, head) slot, `per_tile`
+    distinct random rows inside each 128-query tile (the attention kernel's
+    workgroup), drawn independently per slot, so every workgroup of every
+    head is compared. R = tiles * per_tile (tiles holding fewer rows than
+    per_tile give all of theirs, padded by repeats)."""
+    rng = np.random.default_rng(seed)
+    tiles = -(-n // 128)
+    out = np.empty((heads_total, tiles * per_tile), np.int32)
+    for bh in range(heads_total):
+        for t in range(tiles):
+            lo, hi = 128 * t, min(n, 128 * t + 128)
+            pick = rng.choice(hi - lo, size=per_tile, replace=(hi - lo) < per_tile)
+            out[bh, t * per_tile:(t + 1) * per_tile] = np.sort(lo + pick)
+    return out
+
+
 def gather_rows(o: np.ndarray, rows: np.ndarray) -> np.ndarray:
-    """[B,T,H,D] -> [B,H,R,D] for the given rows."""
-    return np.ascontiguousarray(o[:, rows].transpose(0, 2, 1, 3))
+    """[B,T,H,D] -> [B,H,R,D] for the given rows: a 1-D array shared by every
+    (batch, head), or a [B*H, R] array of per-(batch, head) rows."""
+    if rows.ndim == 1:
+        return np.ascontiguousarray(o[:, rows].transpose(0, 2, 1, 3))
+    B, _, H, D = o.shape
+    r = rows.reshape(B, H, -1)
+    b = np.arange(B)[:, None, None]
+    h = np.arange(H)[None, :, None]
+    return np.ascontiguousarray(o[b, r, h])

@@ -14,7 +14,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from sage_gpu_helpers import assert_prologue_equal, gather_rows, run, sample_rows
+from sage_gpu_helpers import assert_prologue_equal, gather_rows, run, sample_rows, tile_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -51,16 +51,23 @@ SMALL = ["c1", "d128_tail200", "d64_t3001", "d128_gqa", "d64_nosmooth", "d128_ca
          "n1", "n65", "tokens_x10", "outlier_ch20", "d128_causal_b2_xcd", "d64_causal_b2_xcd"]
 
 
-def _check_attention(oracle, p, pro_oracle, o_gpu, rows, q, k, v, label):
+def _check_attention(oracle, p, pro_oracle, o_gpu, rows, q, k, v, label, rows_f64=None):
+    """The north-star gate against the emulator on `rows`, and the comparison
+    with f64 attention on `rows_f64` (default: the same rows). Rows are a 1-D
+    array shared by every (batch, head) or a [B*H, R] array per (batch, head)."""
     emu, emu16 = oracle.sage_emulate(p, pro_oracle, rows=rows, out_dtype=p.dtype)
     ours = oracle.decode16(gather_rows(o_gpu, rows), p.dtype)
     ref = oracle.decode16(emu16, p.dtype)
     e = oracle.errors(ours, ref)
-    exact = oracle.attention_f64(p, q, k, v, rows=rows)
+    assert np.isfinite(ours).all()
+    if rows_f64 is not None:
+        _, emu16 = oracle.sage_emulate(p, pro_oracle, rows=rows_f64, out_dtype=p.dtype)
+        ours = oracle.decode16(gather_rows(o_gpu, rows_f64), p.dtype)
+        ref = oracle.decode16(emu16, p.dtype)
+    exact = oracle.attention_f64(p, q, k, v, rows=rows if rows_f64 is None else rows_f64)
     e64 = oracle.errors(ours, exact)
     emu64 = oracle.errors(ref, exact)
     print(f"{label}: vs reference arithmetic {e}; vs f64 {e64}; reference arithmetic vs f64 {emu64}")
-    assert np.isfinite(ours).all()
     assert e["cos"] >= COS_MIN and e["max_abs"] <= MAX_ABS, e
     assert e64["cos"] >= emu64["cos"] - COS_SLACK, (e64, emu64)
     assert e64["rel_l2"] <= emu64["rel_l2"] * 1.02 + REL_L2_SLACK, (e64, emu64)
@@ -101,14 +108,22 @@ def test_fp16_output_from_bf16_inputs(oracle, torch_gpu):
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
 def test_baseline_configs(oracle, torch_gpu, cfg):
     """The benchmark configurations C1-C5 at full size: prologue bit-exact over every
-    element; attention on sampled rows of every (batch, head)."""
+    element. Attention at the north-star gate on every query row at C1, C2 and C4,
+    and at C3 and C5 on rows drawn per (batch, head) inside every 128-query tile
+    (2 and 1 a tile), so every workgroup of every head is compared; against f64
+    on one row per tile of every head."""
     p, g = oracle.config(cfg, seed=100 + cfg)
     q, k, v = oracle.generate(p, g)
     pro, o = run(torch_gpu, p, q, k, v)
     want = oracle.prologue(p, q, k, v)
     assert_prologue_equal(pro, want)
-    rows = sample_rows(p.tokens, 256 if cfg == 1 else 64, seed=cfg)
-    _check_attention(oracle, p, want, o, rows, q, k, v, f"config {cfg}")
+    bh = p.batch * p.heads
+    if cfg in (1, 2, 4):
+        rows = np.arange(p.tokens, dtype=np.int32)
+    else:
+        rows = tile_rows(p.tokens, bh, per_tile=2 if cfg == 3 else 1, seed=cfg)
+    rows_f64 = tile_rows(p.tokens, bh, per_tile=1, seed=1000 + cfg)
+    _check_attention(oracle, p, want, o, rows, q, k, v, f"config {cfg}", rows_f64=rows_f64)
 
 
 def test_constant_channels_come_out_exactly(oracle, torch_gpu):
@@ -122,3 +137,21 @@ def test_constant_channels_come_out_exactly(oracle, torch_gpu):
     v[..., 77] = c[1]
     _, o = run(torch_gpu, p, q, k, v, want_ws=False)
     assert (o[..., 5] == c[0]).all() and (o[..., 77] == c[1]).all()
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_reference_tiles_give_identical_outputs(oracle, torch_gpu, d):
+    """Every tile the reference accepts (Tile::validate, mod.rs:158-167) runs; the
+    reference's own defaults (Tile::DEFAULT {4,2,3}, Tile::D128 {4,1,3}) and other
+    accepted tiles give bit-identical codes and outputs (the tile only tunes)."""
+    import spl_sage as S
+
+    p, g = oracle.Problem(1, 4, 333, d, kv_heads=2, causal=True), oracle.GenSpec(k_off_std=2.0, seed=31)
+    q, k, v = oracle.generate(p, g)
+    pro0, o0 = run(torch_gpu, p, q, k, v)
+    assert S.Config.for_head_dim(d).tile == (S.Tile.D128 if d == 128 else S.Tile.DEFAULT)
+    for tile in (S.Tile(4, 2, 3), S.Tile(4, 1, 3), S.Tile(8, 1, 4), S.Tile(2, 4, 6), S.Tile(2, 1, 2)):
+        pro, o = run(torch_gpu, p, q, k, v, tile=tile)
+        assert_prologue_equal(pro, pro0)
+        assert np.array_equal(o, o0), tile
+    assert_prologue_equal(pro0, oracle.prologue(p, q, k, v))

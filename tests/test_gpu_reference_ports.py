@@ -1,8 +1,8 @@
-"""The reference's GPU tests (sezer-muhammed/sota-papers-lab,
+"""The reference's dense GPU tests (sezer-muhammed/sota-papers-lab,
 platform/spl-nn/src/sage/tests.rs:597-729), ported to the HIP path on the
 reference's own test data (Data::synthetic, tests.rs:300-329), with the
-reference's gates. KV merging, the fused QK LayerNorm and FP16 P.V
-accumulation are not in this build, so their variants are left out."""
+reference's gates. Their KV-merge, QK LayerNorm and FP16 P.V variants are
+ported in test_gpu_merge.py, test_gpu_qknorm.py and test_gpu_pv16.py."""
 from __future__ import annotations
 
 import numpy as np
@@ -36,6 +36,25 @@ def test_gpu_attention_has_no_spill(torch_gpu):
         regs, spill = S.SageAttention(None, d).attn_resources()
         print(f"d {d}: {regs} VGPRs, {spill} scratch bytes")
         assert spill == 0, f"the attention kernel spills at head dim {d}"
+
+
+# Per kernel: the VGPR limit of the waves a SIMD it is built for (512 VGPRs a
+# lane per SIMD, allocated in blocks of 8): 128 for four waves, 168 for three,
+# 256 for two (the merged head-dim-128 kernel).
+KERNEL_VGPR_LIMITS = {(64, "dense"): 128, (64, "causal"): 128, (64, "merged"): 128,
+                      (128, "dense"): 168, (128, "causal"): 168, (128, "merged"): 256}
+
+
+@pytest.mark.parametrize("d,kernel", sorted(KERNEL_VGPR_LIMITS))
+def test_gpu_every_attention_kernel_fits(torch_gpu, d, kernel):
+    """Every attention kernel (dense, causal, merged; both head dims) is free of
+    spills and keeps the waves a SIMD it is built for."""
+    import spl_sage as S
+
+    regs, spill, lds = S.SageAttention(None, d).attn_kernel_resources(kernel)
+    print(f"d {d} {kernel}: {regs} VGPRs, {spill} scratch bytes, {lds} LDS bytes")
+    assert spill == 0, f"the {kernel} attention kernel spills at head dim {d}"
+    assert regs <= KERNEL_VGPR_LIMITS[(d, kernel)], (d, kernel, regs)
 
 
 def test_gpu_attention_keeps_its_occupancy(torch_gpu):

@@ -197,15 +197,41 @@ def test_v8_position_is_the_operand_permutation(S):
         assert pos[k] == 32 * g + 4 * reg + byte
 
 
+def _reference_tile_ok(w: int, m: int, st: int) -> bool:
+    """Tile::validate (mod.rs:158-167), restated."""
+    return w in (2, 4, 8) and m in (1, 2, 4) and 2 <= st <= 6 and 128 % (16 * m * w) == 0
+
+
 def test_tile_menu_and_errors(S):
-    """mod.rs:116-168: the per-head-dim default tile validates; others are refused
-    with the reference's message."""
-    for d in (64, 128):
-        cfg = S.Config.for_head_dim(d)
-        cfg.tile.validate()
-        assert cfg.tile.rows() == 128
-    with pytest.raises(S.SageError, match="unsupported sage tile"):
-        S.Tile(3, 1, 2).validate()
+    """mod.rs:116-168: exactly the tiles the reference accepts validate; every
+    other tile is refused with the reference's message, which names it."""
+    accepted = 0
+    for w in range(0, 10):
+        for m in range(0, 6):
+            for st in range(0, 8):
+                t = S.Tile(w, m, st)
+                if _reference_tile_ok(w, m, st):
+                    t.validate()
+                    accepted += 1
+                else:
+                    with pytest.raises(S.SageError, match=r"unsupported sage tile Tile \{ warps: %d, m_tiles: %d, "
+                                       r"stages: %d \}" % (w, m, st)):
+                        t.validate()
+    # (2,1), (2,2), (2,4), (4,1), (4,2), (8,1) with stages 2..6
+    assert accepted == 6 * 5
+    for t in (S.Tile(4, 4, 3), S.Tile(8, 2, 3), S.Tile(8, 1, 7), S.Tile(4, 1, 1), S.Tile(3, 1, 2)):
+        with pytest.raises(S.SageError, match="unsupported sage tile"):
+            t.validate()
+
+
+def test_default_tiles_are_the_references(S):
+    """Tile::DEFAULT {4,2,3} and Tile::D128 {4,1,3} (mod.rs:128-147); Config::for_head_dim
+    picks D128 above head dim 64 (mod.rs:141-147, 194-200) with PvAccum::F32."""
+    assert S.Tile.DEFAULT == S.Tile(4, 2, 3) and S.Tile.D128 == S.Tile(4, 1, 3)
+    assert S.Config.for_head_dim(64) == S.Config(S.Tile(4, 2, 3), S.PvAccum.F32)
+    assert S.Config.for_head_dim(128) == S.Config(S.Tile(4, 1, 3), S.PvAccum.F32)
+    assert S.Tile.for_head_dim(64) == S.Tile.DEFAULT and S.Tile.for_head_dim(128) == S.Tile.D128
+    assert S.Tile.DEFAULT.rows() == 128 and S.Tile.D128.rows() == 64
 
 
 def test_device_gate_without_a_gpu(S):
