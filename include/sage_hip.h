@@ -256,6 +256,22 @@ sage_status sage_attend(const sage_attention* s, const sage_workspace* ws, const
 sage_status sage_forward(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,
                          const sage_tensor* v, const sage_tensor_mut* out, const sage_options* opts);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): sage_forward (prepare then attend) for `shape` and
+ * `merge` (NULL = dense) with no workspace. Its buffers are carved from one
+ * device array of SAGE_NOALLOC_MAX_BYTES that the library holds on every GPU
+ * it runs on until the process ends; it allocates and frees nothing. A shape
+ * whose buffers (sage_workspace_bytes of its workspace, each buffer rounded up
+ * to 256 bytes) exceed that is refused with SAGE_ERR_INVALID before any
+ * launch. Every call on one GPU shares that GPU's array: calls whose kernels
+ * can overlap on one GPU (different streams with no ordering between them)
+ * race, so order them on one stream. Outputs equal sage_forward's. */
+#define SAGE_NOALLOC_MAX_BYTES (128ull << 20)
+sage_status sage_forward_noalloc(const sage_attention* s, const sage_shape* shape, const sage_kv_merge* merge,
+                                 const sage_tensor* q, const sage_tensor* k, const sage_tensor* v,
+                                 const sage_tensor_mut* out, const sage_options* opts);
+
 /* Byte position of key k (0..63) of a 64-key block inside each channel row
  * of the v8 layout (the CDNA4 counterpart of sg_vpos, sage_common.cu:151-155):
  * the order in which the QK^T accumulator of the 32x32 MFMA hands keys to the

@@ -353,6 +353,19 @@ public:
         attend(ws, out);
     }
 
+    // forward without a workspace (sage_forward_noalloc; no counterpart in the
+    // reference): the buffers come from the library's fixed per-GPU scratch
+    // array, nothing is allocated; calls that can overlap on one GPU race.
+    void forward_noalloc(const Shape& shape, const Tensor& q, const Tensor& k, const Tensor& v, const TensorMut& out,
+                         const Options& opts = {}, const KvMerge& merge = KvMerge{}) const {
+        const sage_shape sh = shape.raw();
+        const sage_kv_merge m = merge.raw();
+        const sage_tensor tq = q.raw(), tk = k.raw(), tv = v.raw();
+        const sage_tensor_mut to = out.raw();
+        const sage_options o = opts.raw();
+        check(sage_forward_noalloc(h_, &sh, &m, &tq, &tk, &tv, &to, &o));
+    }
+
     // MFMA peak probe (the analogue of sage_peak.cu): which = 0 INT8, 1 FP8,
     // 2 BF16; synchronises and returns dense TOPS.
     double peak(int which, int iters = 2048) const {

@@ -36,7 +36,7 @@ COMMON = [
 PER_FILE = {
     "sage_prologue.hip": ["-ffp-contract=off"],
 }
-SOURCES = ["sage_prologue.hip", "sage_attention.hip", "sage_peak.hip", "sage_api.cpp"]
+SOURCES = ["sage_prologue.hip", "sage_attention.hip", "sage_peak.hip", "sage_noalloc.hip", "sage_api.cpp"]
 
 
 def _compile(src: str) -> Path:
@@ -57,7 +57,7 @@ def _compile(src: str) -> Path:
 def build(verbose: bool = True) -> Path:
     """Compile and link; returns the library path. Raises on failure."""
     OBJ.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
+    with ThreadPoolExecutor(max_workers=min(5, len(SOURCES))) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", *map(str, objs), "-o", str(tmp)]

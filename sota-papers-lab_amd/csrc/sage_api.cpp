@@ -98,13 +98,6 @@ uint64_t kv_heads_of(const sage_shape& s) { return s.kv_heads ? s.kv_heads : s.h
 
 }  // namespace
 
-struct sage_attention {
-    hipStream_t stream;
-    int device;
-    uint64_t head_dim;
-    sage_config config;
-};
-
 struct sage_workspace {
     sage_plan plan;
     uint64_t head_dim;
@@ -299,10 +292,22 @@ static void ws_free(sage_workspace* w) {
         if (p) (void)hipFree(p);
 }
 
-sage_status sage_workspace_new(const sage_attention* s, const sage_shape* shape, const sage_kv_merge* merge,
-                           sage_workspace** out) {
-    if (!s || !shape || !out) return fail(SAGE_ERR_INVALID, "null argument");
-    *out = nullptr;
+}  // extern "C"
+
+namespace sage {
+
+sage_status set_error(sage_status st, const char* fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return st;
+}
+
+sage_status workspace_layout(const sage_attention* s, const sage_shape* shape, const sage_kv_merge* merge,
+                             sage_plan* plan_out, WsSizes* n) {
     sage_kv_merge dense{};
     dense.stride = 1;
     sage_plan plan;
@@ -322,18 +327,42 @@ sage_status sage_workspace_new(const sage_attention* s, const sage_shape* shape,
                        __builtin_add_overflow(total, n_k8, &total) || total > (1ull << 62);
     if (wraps)
         return fail(SAGE_ERR_INVALID, "sage workspace for %s is too large to address", shape_dbg(*shape).c_str());
+    n->q8 = n_q8;
+    n->q_scale = b * h * plan.tq_pad / SAGE_QGROUP;
+    n->k8 = n_k8;
+    n->k_scale = b * hk * plan.tk_pad / SAGE_KBLOCK;
+    n->v8 = n_k8;
+    n->stats = b * hk * 4 * d;
+    n->kbias = plan.tk_pad;
+    n->part = n_part;
+    *plan_out = plan;
+    return SAGE_OK;
+}
+
+}  // namespace sage
+
+extern "C" {
+
+sage_status sage_workspace_new(const sage_attention* s, const sage_shape* shape, const sage_kv_merge* merge,
+                           sage_workspace** out) {
+    if (!s || !shape || !out) return fail(SAGE_ERR_INVALID, "null argument");
+    *out = nullptr;
+    sage_plan plan;
+    sage::WsSizes n;
+    sage_status st = sage::workspace_layout(s, shape, merge, &plan, &n);
+    if (st != SAGE_OK) return st;
     sage_workspace* w = new sage_workspace;
     w->plan = plan;
-    w->head_dim = d;
+    w->head_dim = s->head_dim;
     w->device = s->device;
-    w->n_q8 = n_q8;
-    w->n_q_scale = b * h * plan.tq_pad / SAGE_QGROUP;
-    w->n_k8 = n_k8;
-    w->n_k_scale = b * hk * plan.tk_pad / SAGE_KBLOCK;
-    w->n_v8 = n_k8;
-    w->n_stats = b * hk * 4 * d;
-    w->n_kbias = plan.tk_pad;
-    w->n_part = n_part;
+    w->n_q8 = n.q8;
+    w->n_q_scale = n.q_scale;
+    w->n_k8 = n.k8;
+    w->n_k_scale = n.k_scale;
+    w->n_v8 = n.v8;
+    w->n_stats = n.stats;
+    w->n_kbias = n.kbias;
+    w->n_part = n.part;
     struct {
         void** p;
         uint64_t bytes;
@@ -405,13 +434,13 @@ static sage_status check_tensor(const sage_strides& st, const void* data, uint64
     return SAGE_OK;
 }
 
-sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,
-                         const sage_tensor* v, const sage_options* opts) {
-    if (!s || !ws || !q || !k || !v || !opts) return fail(SAGE_ERR_INVALID, "null argument");
-    if (ws->head_dim != s->head_dim)
-        return fail(SAGE_ERR_INVALID, "workspace was made for head dim %llu, kernels are %llu", (u64)ws->head_dim,
-                    (u64)s->head_dim);
-    const sage_plan& plan = ws->plan;
+}  // extern "C"
+
+namespace sage {
+
+sage_status prepare_view(const sage_attention* s, const WsView& w, const sage_tensor* q, const sage_tensor* k,
+                         const sage_tensor* v, const sage_options* opts, Geom* geom) {
+    const sage_plan& plan = w.plan;
     const uint64_t d = s->head_dim;
     const struct {
         const sage_tensor* t;
@@ -433,15 +462,15 @@ sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage
     if (opts->causal && plan.merge.stride != 1)
         return fail(SAGE_ERR_UNSUPPORTED, "causal masking over merged keys (KvMerge::Pool) is not supported");
     int flags = 0;
-    if (opts->qk_norm_params) flags |= sage::F_LN_Q | sage::F_LN_K;  // mod.rs:715-717
-    if (opts->smooth_k) flags |= sage::F_SMOOTH_K;
-    if (opts->smooth_v) flags |= sage::F_SMOOTH_V;
-    if (opts->causal) flags |= sage::F_CAUSAL;
-    if (q->dtype == SAGE_F16) flags |= sage::F_IN_F16;
+    if (opts->qk_norm_params) flags |= F_LN_Q | F_LN_K;  // mod.rs:715-717
+    if (opts->smooth_k) flags |= F_SMOOTH_K;
+    if (opts->smooth_v) flags |= F_SMOOTH_V;
+    if (opts->causal) flags |= F_CAUSAL;
+    if (q->dtype == SAGE_F16) flags |= F_IN_F16;
     const float scale = opts->has_softmax_scale ? opts->softmax_scale : 1.0f / std::sqrt((float)d);
     const float log2e = 1.44269504088896340736f;
 
-    sage::Geom g{};
+    Geom g{};
     g.q_sb = (long long)q->strides.batch;
     g.q_st = (long long)q->strides.token;
     g.q_sh = (long long)q->strides.head;
@@ -482,11 +511,48 @@ sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage
         g.dense_frames = (int)(l.dense_frames < l.frames ? l.dense_frames : l.frames);
     }
 
-    sage::PrologueBufs bufs{ws->q8, ws->q_scale, ws->k8, ws->k_scale, ws->v8, ws->stats, ws->part, ws->kbias};
-    hipError_t e = sage::launch_prologue((int)d, static_cast<const uint16_t*>(q->data),
-                                         static_cast<const uint16_t*>(k->data), static_cast<const uint16_t*>(v->data),
-                                         opts->qk_norm_params, bufs, g, s->stream);
+    PrologueBufs bufs{w.q8, w.q_scale, w.k8, w.k_scale, w.v8, w.stats, w.part, w.kbias};
+    hipError_t e = launch_prologue((int)d, static_cast<const uint16_t*>(q->data), static_cast<const uint16_t*>(k->data),
+                                   static_cast<const uint16_t*>(v->data), opts->qk_norm_params, bufs, g, s->stream);
     if (e != hipSuccess) return hip_fail(e, "launch sage prologue");
+    *geom = g;
+    return SAGE_OK;
+}
+
+sage_status attend_view(const sage_attention* s, const WsView& w, const Geom& geom, const sage_tensor_mut* out) {
+    const sage_plan& plan = w.plan;
+    sage_status r = check_tensor(out->strides, out->data, out->len, plan, plan.shape.heads, s->head_dim, "output");
+    if (r != SAGE_OK) return r;
+    if (out->dtype != SAGE_BF16 && out->dtype != SAGE_F16)
+        return fail(SAGE_ERR_INVALID, "unknown dtype %d", out->dtype);
+    Geom g = geom;
+    g.o_sb = (long long)out->strides.batch;
+    g.o_st = (long long)out->strides.token;
+    g.o_sh = (long long)out->strides.head;
+    g.flags = (g.flags & ~F_OUT_F16) | (out->dtype == SAGE_F16 ? F_OUT_F16 : 0);
+    AttendBufs bufs{w.q8, w.q_scale, w.k8, w.k_scale, w.v8, w.stats, w.kbias, out->data};
+    hipError_t e = launch_attention((int)s->head_dim, bufs, g, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "launch sage attention");
+    return SAGE_OK;
+}
+
+}  // namespace sage
+
+extern "C" {
+
+static sage::WsView view_of(const sage_workspace* w) {
+    return sage::WsView{w->plan, w->q8, w->q_scale, w->k8, w->k_scale, w->v8, w->stats, w->kbias, w->part};
+}
+
+sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,
+                         const sage_tensor* v, const sage_options* opts) {
+    if (!s || !ws || !q || !k || !v || !opts) return fail(SAGE_ERR_INVALID, "null argument");
+    if (ws->head_dim != s->head_dim)
+        return fail(SAGE_ERR_INVALID, "workspace was made for head dim %llu, kernels are %llu", (u64)ws->head_dim,
+                    (u64)s->head_dim);
+    sage::Geom g;
+    sage_status r = sage::prepare_view(s, view_of(ws), q, k, v, opts, &g);
+    if (r != SAGE_OK) return r;
     ws->geom = g;
     ws->prepared = true;
     return ok();
@@ -498,20 +564,8 @@ sage_status sage_attend(const sage_attention* s, const sage_workspace* ws, const
     if (ws->head_dim != s->head_dim)
         return fail(SAGE_ERR_INVALID, "workspace was made for head dim %llu, kernels are %llu", (u64)ws->head_dim,
                     (u64)s->head_dim);
-    const sage_plan& plan = ws->plan;
-    sage_status r = check_tensor(out->strides, out->data, out->len, plan, plan.shape.heads, s->head_dim, "output");
-    if (r != SAGE_OK) return r;
-    if (out->dtype != SAGE_BF16 && out->dtype != SAGE_F16)
-        return fail(SAGE_ERR_INVALID, "unknown dtype %d", out->dtype);
-    sage::Geom g = ws->geom;
-    g.o_sb = (long long)out->strides.batch;
-    g.o_st = (long long)out->strides.token;
-    g.o_sh = (long long)out->strides.head;
-    g.flags = (g.flags & ~sage::F_OUT_F16) | (out->dtype == SAGE_F16 ? sage::F_OUT_F16 : 0);
-    sage::AttendBufs bufs{ws->q8, ws->q_scale, ws->k8, ws->k_scale, ws->v8, ws->stats, ws->kbias, out->data};
-    hipError_t e = sage::launch_attention((int)s->head_dim, bufs, g, s->stream);
-    if (e != hipSuccess) return hip_fail(e, "launch sage attention");
-    return ok();
+    sage_status r = sage::attend_view(s, view_of(ws), ws->geom, out);
+    return r == SAGE_OK ? ok() : r;
 }
 
 sage_status sage_forward(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,

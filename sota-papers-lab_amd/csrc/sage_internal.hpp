@@ -4,6 +4,16 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/sage_hip.h"
+
+// SageAttention (mod.rs:509-520): the context behind the C ABI's handle.
+struct sage_attention {
+    hipStream_t stream;
+    int device;
+    uint64_t head_dim;
+    sage_config config;
+};
+
 namespace sage {
 
 struct Geom;
@@ -48,5 +58,39 @@ hipError_t attention_resources(int head_dim, bool causal, bool merge, int* regs,
 
 // MFMA peak probe: which 0 = INT8, 1 = FP8, 2 = BF16; returns dense TOPS.
 hipError_t run_peak(int which, int iters, hipStream_t s, double* tops);
+
+// Element counts of a workspace's buffers.
+struct WsSizes {
+    uint64_t q8, q_scale, k8, k_scale, v8, stats, kbias, part;
+};
+
+// A workspace's buffers: owned by a sage_workspace, or carved from the
+// no-allocation entry point's scratch array.
+struct WsView {
+    sage_plan plan;
+    int8_t* q8;
+    float* q_scale;
+    int8_t* k8;
+    float* k_scale;
+    uint8_t* v8;
+    float* stats;
+    float* kbias;
+    float* part;
+};
+
+// Sets this thread's sage_last_error() text; returns st.
+sage_status set_error(sage_status st, const char* fmt, ...);
+
+// Plan::new plus the buffer sizes of SageAttention::workspace for shape and
+// merge (NULL = dense), with the same refusals.
+sage_status workspace_layout(const sage_attention* s, const sage_shape* shape, const sage_kv_merge* merge,
+                             sage_plan* plan, WsSizes* n);
+
+// The bodies of prepare and attend on a buffer view: every check before any
+// launch, then the launches on s->stream. prepare_view returns the kernel
+// parameters attend_view needs.
+sage_status prepare_view(const sage_attention* s, const WsView& w, const sage_tensor* q, const sage_tensor* k,
+                         const sage_tensor* v, const sage_options* opts, Geom* geom);
+sage_status attend_view(const sage_attention* s, const WsView& w, const Geom& geom, const sage_tensor_mut* out);
 
 }  // namespace sage

@@ -70,6 +70,8 @@ class Tile:
         return Config.for_head_dim(head_dim).tile
 
 
+NOALLOC_MAX_BYTES = 128 << 20  # SAGE_NOALLOC_MAX_BYTES
+
 Tile.DEFAULT = Tile(4, 2, 3)  # mod.rs:128-132
 Tile.D128 = Tile(4, 1, 3)  # mod.rs:136-140
 
@@ -486,6 +488,15 @@ class SageAttention:
                 opts: Optional[Options] = None) -> None:
         self.prepare(ws, q, k, v, opts)
         self.attend(ws, out)
+
+    def forward_noalloc(self, shape: Shape, q: Tensor, k: Tensor, v: Tensor, out: TensorMut,
+                        opts: Optional[Options] = None, merge: KvMerge = KvMerge.Dense) -> None:
+        """forward without a workspace (sage_forward_noalloc): the buffers come
+        from the library's fixed per-GPU scratch array (NOALLOC_MAX_BYTES); no
+        device memory is allocated. Calls that can overlap on one GPU race."""
+        o = (opts or Options())._c()
+        _check(lib().sage_forward_noalloc(self._h, C.byref(shape._c()), C.byref(merge._c()), C.byref(q._c()),
+                                          C.byref(k._c()), C.byref(v._c()), C.byref(out._c()), C.byref(o)))
 
     def peak(self, which: int, iters: int = 2048) -> float:
         """Measured dense TOPS of one MFMA shape (0 INT8, 1 FP8, 2 BF16)."""

@@ -109,6 +109,11 @@ SIGNATURES = {
         i32,
         [C.c_void_p, C.c_void_p, P(sage_tensor), P(sage_tensor), P(sage_tensor), P(sage_tensor_mut), P(sage_options)],
     ),
+    "sage_forward_noalloc": (
+        i32,
+        [C.c_void_p, P(sage_shape), P(sage_kv_merge), P(sage_tensor), P(sage_tensor), P(sage_tensor),
+         P(sage_tensor_mut), P(sage_options)],
+    ),
     "sage_v8_position": (i32, [i32]),
     "sage_peak": (i32, [C.c_void_p, i32, i32, P(C.c_double)]),
 }
