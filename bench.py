@@ -14,8 +14,10 @@ reference's attn_tops (tests.rs:968-971). One GPU only.
 
 prints, instead of the headline line, the reference's own gpu_bench workload
 (tests.rs:817-990: VGGT-Omega global attention, B1 H16 D64, 689-token frames)
-in the chosen mode. `--only attend|prepare|copy` times one kernel group (for
-the profiler).
+in the chosen mode. `--qkv` puts the upstream QKV prologue in front of the
+chosen configuration and times the reference's two steps against the fused
+prepare_qkv. `--only attend|prepare|copy` times one kernel group (for the
+profiler).
 """
 from __future__ import annotations
 
@@ -225,6 +227,84 @@ def vggt_bench(args, torch, S) -> int:
     return 0
 
 
+def qkv_bench(args, torch, S) -> int:
+    """The upstream QKV prologue (qkv.rs, qkv.cu) in front of the chosen
+    configuration: the fused projection y (bf16 [B][N][(H + 2 HKV) * D]) with
+    per-channel scales and bias, LayerNorm QK-norm and 2D RoPE (VGGT layout
+    over a 64-column patch grid). Times, per step, the two-step path the
+    reference runs -- QkvPrologue::run writing bf16 Q, K and V, then prepare
+    and attend -- against the fused prepare_qkv + attend, which never writes
+    or re-reads Q, K and V in bf16. Prints one JSON line."""
+    from spl_sage import qkv as Q
+
+    B, H, HK, N, D, dt, causal, *_ = CONFIGS[args.config]
+    g = torch.Generator(device="cuda").manual_seed(0)
+    width = (H + 2 * HK) * D
+    y = (torch.randn((B, N, width), generator=g, device="cuda")
+         + 0.5 * torch.randn((width,), generator=g, device="cuda")).to(torch.bfloat16)
+    chan = (0.5 + torch.rand((width,), generator=g, device="cuda")).float()
+    bias = (0.2 * torch.randn((width,), generator=g, device="cuda")).to(torch.bfloat16)
+    nw = [(1 + 0.2 * torch.randn((D,), generator=g, device="cuda")).float(),
+          (0.1 * torch.randn((D,), generator=g, device="cuda")).float(),
+          (1 + 0.2 * torch.randn((D,), generator=g, device="cuda")).float(),
+          (0.1 * torch.randn((D,), generator=g, device="cuda")).float()]
+    gw = 64
+    table = Q.RopeTable.vggt((N + gw - 1) // gw, gw, 0, 100.0, D)
+    rope = Q.Rope(table.upload(), Q.RopeLayout.Vggt, table.frame_len)
+    norm = Q.QkNorm(Q.NormKind.LayerNorm, nw[0], nw[2], nw[1], nw[3], 1e-6)
+    inp = Q.QkvIn(y, width, chan=chan, bias=bias)
+    stream = torch.cuda.current_stream()
+    sa = S.SageAttention(stream, D)
+    ws = sa.workspace(S.Shape(B, H, N, HK if HK != H else 0))
+    out = torch.empty((B, N, H, D), dtype=torch.bfloat16, device="cuda")
+    q = torch.empty((B, N, H, D), dtype=torch.bfloat16, device="cuda")
+    k = torch.empty((B, N, HK, D), dtype=torch.bfloat16, device="cuda")
+    v = torch.empty_like(k)
+    pro = Q.QkvPrologue(sa)
+    qo = Q.QkvOut(S.TensorMut(q), S.TensorMut(k), S.TensorMut(v))
+    opts = S.Options(causal=causal)
+    ot = S.TensorMut(out)
+
+    def qkv_only():
+        pro.run(inp, N, H, norm, rope, qo, batch=B, kv_heads=HK if HK != H else 0)
+
+    def two_step():
+        qkv_only()
+        sa.forward(ws, S.Tensor(q), S.Tensor(k), S.Tensor(v), ot, opts)
+
+    def fused():
+        sa.forward_qkv(ws, inp, ot, norm, rope, opts)
+
+    def prepare_fused():
+        sa.prepare_qkv(ws, inp, norm, rope, opts)
+
+    def prepare_plain():
+        sa.prepare(ws, S.Tensor(q), S.Tensor(k), S.Tensor(v), opts)
+
+    for _ in range(args.warmup):
+        two_step()
+        fused()
+    torch.cuda.synchronize()
+    reps = max(args.steps, 20)
+    t2 = time_median(torch, stream, two_step, reps)[0]
+    t1 = time_median(torch, stream, fused, reps)[0]
+    tq = time_median(torch, stream, qkv_only, reps)[0]
+    tpf = time_median(torch, stream, prepare_fused, reps)[0]
+    tpp = time_median(torch, stream, prepare_plain, reps)[0]
+    ops = S.flops(ws.plan(), D, causal)
+    y_bytes = B * N * width * 2
+    print(json.dumps({
+        "workload": f"QKV prologue + sage, {NAMES[args.config]} (LayerNorm QK-norm, VGGT RoPE, channel scales, bias)",
+        "two_step_ms": round(t2, 4), "fused_ms": round(t1, 4), "speedup": round(t2 / t1, 3),
+        "qkv_prologue_ms": round(tq, 4), "prepare_from_bf16_ms": round(tpp, 4), "prepare_qkv_ms": round(tpf, 4),
+        "qkv_prologue_gbs": round(2 * y_bytes / (tq * 1e-3) / 1e9, 1),
+        "bf16_round_trip_bytes": 2 * y_bytes,
+        "two_step_tops": round(ops / (t2 * 1e-3) / 1e12, 1), "fused_tops": round(ops / (t1 * 1e-3) / 1e12, 1),
+        "timing": "median of individually event-timed calls",
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -241,6 +321,9 @@ def main() -> int:
     ap.add_argument("--merge", type=int, default=1, choices=[1, 2, 4], help="--vggt: KV merge stride (1 = dense)")
     ap.add_argument("--pv16", action="store_true", help="--vggt: PvAccum::F16")
     ap.add_argument("--qk-norm", action="store_true", help="--vggt: fused QK LayerNorm")
+    ap.add_argument("--qkv", action="store_true",
+                    help="instead of the headline line: the upstream QKV prologue in front of --config, the "
+                         "reference's two steps against the fused prepare_qkv")
     ap.add_argument("--only", choices=["attend", "prepare", "copy"],
                     help="profiling mode: run only this kernel group --steps times and print its timing "
                          "(copy: a plain 512 MiB device copy, the reference for HBM byte counters)")
@@ -256,6 +339,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.vggt:
         return vggt_bench(args, torch, S)
+    if args.qkv:
+        return qkv_bench(args, torch, S)
     if args.only == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)

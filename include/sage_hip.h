@@ -256,6 +256,93 @@ sage_status sage_attend(const sage_attention* s, const sage_workspace* ws, const
 sage_status sage_forward(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,
                          const sage_tensor* v, const sage_tensor_mut* out, const sage_options* opts);
 
+/* ---- The QKV prologue (platform/spl-nn/src/qkv.rs, cuda/qkv.cu) ----
+ * The step before sage in the reference's transformer block: it splits the
+ * fused QKV projection, applies its optional dequantisation scales and bias,
+ * QK-norm (LayerNorm or RMSNorm over the head dim, weights shared across
+ * heads) and 2D RoPE on q and k, and writes bf16 Q, K and V. Head dim 64 is
+ * the reference's; 128 is an extension (the same arithmetic, RoPE pairs D/4
+ * or D/2 apart). */
+
+/* QkvIn (qkv.rs:165-177) with a batch dimension: y is bf16 rows of `ld`
+ * elements per token (batch items batch_stride elements apart; 0 = tokens *
+ * ld), holding q | k | v of heads*D, kv_heads*D and kv_heads*D channels
+ * (kv_heads from the shape; equal to heads in the reference). tok: f32
+ * [batch * tokens] per-token scales; chan: f32 [(heads + 2 kv_heads) * D]
+ * per-channel scales; bias: bf16 [(heads + 2 kv_heads) * D]; NULL = none.
+ * The *_len fields give each buffer's element count. */
+typedef struct sage_qkv_in {
+    const void* y;
+    uint64_t y_len;
+    uint64_t ld;
+    uint64_t batch_stride;
+    const float* tok;
+    uint64_t tok_len;
+    const float* chan;
+    uint64_t chan_len;
+    const uint16_t* bias;
+    uint64_t bias_len;
+} sage_qkv_in;
+
+/* NormKind (qkv.rs:138-143) and QkNorm (qkv.rs:145-156): f32 [D] weights
+ * (len elements each), biases used (and required) by LayerNorm only. */
+typedef enum sage_qkv_norm_kind { SAGE_QKV_LAYER_NORM = 1, SAGE_QKV_RMS_NORM = 2 } sage_qkv_norm_kind;
+typedef struct sage_qkv_norm {
+    int32_t kind;
+    const float* q_weight;
+    const float* q_bias;
+    const float* k_weight;
+    const float* k_bias;
+    uint64_t len;
+    float eps;
+} sage_qkv_norm;
+
+/* RopeLayout (qkv.rs:33-58) and Rope (qkv.rs:158-163): table is f32
+ * [frame_len][D/2][2] (cos, sin per rotation pair; table_len elements), row
+ * token % frame_len. VGGT rotates pairs (i, i + D/4) inside each half of the
+ * head, DINOv3 pairs (i, i + D/2). */
+typedef enum sage_rope_layout { SAGE_ROPE_VGGT = 0, SAGE_ROPE_DINOV3 = 1 } sage_rope_layout;
+typedef struct sage_qkv_rope {
+    const float* table;
+    uint64_t table_len;
+    int32_t layout;
+    uint64_t frame_len;
+} sage_qkv_rope;
+
+/* RopeTable::vggt / RopeTable::dinov3 (qkv.rs:87-136), host only: writes the
+ * (special + grid_h * grid_w) x (head_dim / 2) x 2 table (cos, sin of the f64
+ * angle, rounded to f32) to `out`, which holds out_len floats. */
+sage_status sage_rope_table(int32_t layout, uint64_t head_dim, uint64_t grid_h, uint64_t grid_w, uint64_t special,
+                            double base, float* out, uint64_t out_len);
+
+/* QkvPrologue::run (qkv.rs:216-306) on the context's stream: shape gives
+ * batch, heads, kv_heads and tokens; norm and rope may be NULL. Q and K are
+ * written bf16, V bf16 or fp16 (its dtype; VFormat), into [batch][token]
+ * [head][dim] views (any strides that are multiples of 8; the reference's
+ * [heads][tokens][64] is the bhtd view). Refusals carry the reference's text
+ * ("qkv: ld .. must be a multiple of 8 and at least ..", "qkv: LayerNorm
+ * QK-norm needs q and k biases", "qkv: RoPE frame length is 0", "<what>:
+ * buffer holds .. elements, needs ..", "device pointer .. is not 16-byte
+ * aligned"). An empty shape is a no-op, as there. */
+sage_status sage_qkv_prologue(const sage_attention* s, const sage_shape* shape, const sage_qkv_in* in,
+                              const sage_qkv_norm* norm, const sage_qkv_rope* rope, const sage_tensor_mut* q,
+                              const sage_tensor_mut* k, const sage_tensor_mut* v);
+
+/* SageAttention::prepare fed straight from the fused QKV projection (the
+ * fusion of the two steps; no counterpart in the reference, which runs
+ * QkvPrologue::run, stores bf16 Q, K and V and prepares from them): the
+ * workspace receives the codes and scales that QkvPrologue::run followed by
+ * sage_prepare would give, bit for bit, without the bf16 round trip. The
+ * shape is the workspace's; opts as sage_prepare (QkNorm of the sage options
+ * then applies to the QKV prologue's output). */
+sage_status sage_prepare_qkv(const sage_attention* s, sage_workspace* ws, const sage_qkv_in* in,
+                             const sage_qkv_norm* norm, const sage_qkv_rope* rope, const sage_options* opts);
+
+/* sage_prepare_qkv then sage_attend. */
+sage_status sage_forward_qkv(const sage_attention* s, sage_workspace* ws, const sage_qkv_in* in,
+                             const sage_qkv_norm* norm, const sage_qkv_rope* rope, const sage_tensor_mut* out,
+                             const sage_options* opts);
+
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): sage_forward (prepare then attend) for `shape` and

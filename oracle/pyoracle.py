@@ -402,3 +402,141 @@ def config(n: int, seed: int = 1):
         return (Problem(1, 48, 17776, 64, dtype=F16),
                 GenSpec(k_off_std=3.0, token_frac=0.02, token_scale=10.0, seed=seed))
     raise ValueError(n)
+
+
+# ------------------------------------------------------------------ QKV prologue (qkv.cu, qkv.rs)
+
+NORM_NONE, NORM_LAYER, NORM_RMS = 0, 1, 2
+ROPE_VGGT, ROPE_DINOV3 = 0, 1
+
+
+class _Qkv(C.Structure):
+    _fields_ = [
+        ("batch", C.c_int), ("tokens", C.c_int), ("heads", C.c_int), ("kv_heads", C.c_int), ("head_dim", C.c_int),
+        ("ld", C.c_longlong), ("batch_stride", C.c_longlong),
+        ("tok", C.c_void_p), ("chan", C.c_void_p), ("bias", C.c_void_p),
+        ("norm", C.c_int), ("q_w", C.c_void_p), ("q_b", C.c_void_p), ("k_w", C.c_void_p), ("k_b", C.c_void_p),
+        ("eps", C.c_float), ("rope", C.c_void_p), ("rope_layout", C.c_int), ("frame_len", C.c_int),
+        ("v_f16", C.c_int),
+    ]
+
+
+@dataclass
+class QkvSpec:
+    """The fused QKV projection's layout and the qkv_prologue options
+    (qkv.cu:9-31): y is bf16 [batch][tokens][ld], q | k | v of heads*D,
+    kv_heads*D, kv_heads*D channels. Arrays are numpy; None is off. norm_w is
+    [4][D] float32 (q weight, q bias, k weight, k bias); rope is float32
+    [frame_len][D/2][2] (cos, sin)."""
+
+    batch: int
+    tokens: int
+    heads: int
+    head_dim: int
+    kv_heads: int = 0
+    ld: int = 0
+    tok: np.ndarray | None = field(default=None, compare=False)
+    chan: np.ndarray | None = field(default=None, compare=False)
+    bias: np.ndarray | None = field(default=None, compare=False)  # uint16 bf16 codes
+    norm: int = NORM_NONE
+    norm_w: np.ndarray | None = field(default=None, compare=False)
+    eps: float = 1e-6
+    rope: np.ndarray | None = field(default=None, compare=False)
+    rope_layout: int = ROPE_VGGT
+    v_f16: bool = False  # V as f16 codes (VFormat::F16)
+
+    @property
+    def hk(self) -> int:
+        return self.kv_heads or self.heads
+
+    @property
+    def width(self) -> int:
+        return (self.heads + 2 * self.hk) * self.head_dim
+
+    def row_stride(self) -> int:
+        return self.ld or self.width
+
+    def _c(self) -> _Qkv:
+        D = self.head_dim
+        keep = []
+
+        def ptr(a, dt):
+            if a is None:
+                return None
+            a = np.ascontiguousarray(a, dtype=dt)
+            keep.append(a)
+            return a.ctypes.data
+
+        w = None if self.norm_w is None else np.ascontiguousarray(self.norm_w, np.float32).reshape(4, D)
+        if w is not None:
+            keep.append(w)
+        rope = None if self.rope is None else np.ascontiguousarray(self.rope, np.float32)
+        if rope is not None:
+            keep.append(rope)
+        c = _Qkv(self.batch, self.tokens, self.heads, self.hk, D, self.row_stride(),
+                 self.tokens * self.row_stride(), ptr(self.tok, np.float32), ptr(self.chan, np.float32),
+                 ptr(self.bias, np.uint16), int(self.norm),
+                 None if w is None else w[0].ctypes.data, None if w is None else w[1].ctypes.data,
+                 None if w is None else w[2].ctypes.data, None if w is None else w[3].ctypes.data,
+                 float(self.eps), None if rope is None else rope.ctypes.data, int(self.rope_layout),
+                 0 if rope is None else rope.shape[0], int(self.v_f16))
+        c._keep = keep
+        return c
+
+
+def _qkv_lib():
+    l = lib()
+    if not getattr(l, "_qkv_ready", False):
+        vp = C.c_void_p
+        l.oracle_rope_table.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, vp]
+        l.oracle_rope_half.restype = C.c_int
+        l.oracle_rope_half.argtypes = [C.c_int, C.c_int]
+        l.oracle_rope_pair.restype = C.c_int
+        l.oracle_rope_pair.argtypes = [C.c_int, C.c_int, C.c_int]
+        l.oracle_qkv_prologue.argtypes = [C.POINTER(_Qkv), vp, vp, vp, vp]
+        l.oracle_qkv_reference_f64.argtypes = [C.POINTER(_Qkv), vp, vp, vp, vp]
+        l._qkv_ready = True
+    return l
+
+
+def rope_table(layout: int, head_dim: int, grid_h: int, grid_w: int, special: int, base: float = 100.0):
+    """RopeTable::vggt / ::dinov3 (qkv.rs:87-136): float32 [frame_len][D/2][2]."""
+    n = special + grid_h * grid_w
+    out = np.empty((n, head_dim // 2, 2), np.float32)
+    _qkv_lib().oracle_rope_table(layout, head_dim, grid_h, grid_w, special, float(base), _p(out))
+    return out
+
+
+def rope_pair(layout: int, head_dim: int, d: int) -> int:
+    return _qkv_lib().oracle_rope_pair(layout, head_dim, d)
+
+
+def rope_half(layout: int, head_dim: int) -> int:
+    return _qkv_lib().oracle_rope_half(layout, head_dim)
+
+
+def _qkv_out(s: QkvSpec, dtype):
+    D = s.head_dim
+    return (np.empty((s.batch, s.tokens, s.heads, D), dtype), np.empty((s.batch, s.tokens, s.hk, D), dtype),
+            np.empty((s.batch, s.tokens, s.hk, D), dtype))
+
+
+def qkv_prologue(s: QkvSpec, y: np.ndarray):
+    """qkv_prologue's fp32 arithmetic (qkv.cu:37-133): bf16 codes Q [B,T,H,D],
+    K and V [B,T,HKV,D] from y (uint16 bf16 codes [B,T,ld])."""
+    y = np.ascontiguousarray(y, dtype=np.uint16)
+    assert y.shape == (s.batch, s.tokens, s.row_stride())
+    q, k, v = _qkv_out(s, np.uint16)
+    c = s._c()
+    _qkv_lib().oracle_qkv_prologue(C.byref(c), _p(y), _p(q), _p(k), _p(v))
+    return q, k, v
+
+
+def qkv_reference_f64(s: QkvSpec, y: np.ndarray):
+    """qkv::reference (qkv.rs:310-372): the f64 CPU reference, as float32."""
+    y = np.ascontiguousarray(y, dtype=np.uint16)
+    assert y.shape == (s.batch, s.tokens, s.row_stride())
+    q, k, v = _qkv_out(s, np.float32)
+    c = s._c()
+    _qkv_lib().oracle_qkv_reference_f64(C.byref(c), _p(y), _p(q), _p(k), _p(v))
+    return q, k, v

@@ -210,6 +210,40 @@ void oracle_attention_f64_rows(const oracle_problem* p, int causal, float scale,
                                const uint16_t* k, const uint16_t* v, const int* rows, int nrows, int rows_stride,
                                float* out, int threads);
 
+/* ---- QKV prologue (qkv.cu, qkv.rs) ---- */
+enum { ORACLE_NORM_NONE = 0, ORACLE_NORM_LAYER = 1, ORACLE_NORM_RMS = 2 };
+enum { ORACLE_ROPE_VGGT = 0, ORACLE_ROPE_DINOV3 = 1 };
+
+/* The fused QKV projection y (bf16 [batch][tokens] rows of ld elements, batch
+ * items batch_stride apart; q | k | v, heads*D, kv_heads*D, kv_heads*D wide)
+ * and the QkvArgs options of qkv.cu:9-31 (NULL pointers = off). tok is
+ * [batch * tokens]; chan and bias are [(heads + 2 kv_heads) * D]; the norm
+ * parameters [D] each (biases read under LayerNorm only); rope is
+ * [frame_len][D/2][2] (cos, sin). */
+typedef struct {
+    int batch, tokens, heads, kv_heads, head_dim;
+    long long ld, batch_stride;
+    const float* tok;
+    const float* chan;
+    const uint16_t* bias;
+    int norm; /* ORACLE_NORM_* */
+    const float *q_w, *q_b, *k_w, *k_b;
+    float eps;
+    const float* rope;
+    int rope_layout; /* ORACLE_ROPE_* */
+    int frame_len;
+    int v_f16; /* V written as f16 codes of its fp32 value (VFormat::F16) */
+} oracle_qkv;
+
+int oracle_rope_half(int layout, int D);
+int oracle_rope_pair(int layout, int D, int d);
+void oracle_rope_table(int layout, int D, int grid_h, int grid_w, int special, double base, float* out);
+/* qkv_prologue's fp32 arithmetic, bf16 outputs Q [b][t][heads][D], K and V
+ * [b][t][kv_heads][D]. */
+void oracle_qkv_prologue(const oracle_qkv* a, const uint16_t* y, uint16_t* q, uint16_t* k, uint16_t* v);
+/* qkv::reference (qkv.rs:310-372) in f64, outputs rounded to f32, same layouts. */
+void oracle_qkv_reference_f64(const oracle_qkv* a, const uint16_t* y, float* q, float* k, float* v);
+
 /* Errors of `ours` against `ref` (reference.rs:202-225):
  * out[0] cos, [1] rel_l1, [2] rel_l2, [3] max_abs, [4] ref_max. */
 void oracle_errors(const float* ours, const float* ref, size_t n, double* out);

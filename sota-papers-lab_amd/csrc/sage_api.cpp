@@ -439,7 +439,7 @@ static sage_status check_tensor(const sage_strides& st, const void* data, uint64
 namespace sage {
 
 sage_status prepare_view(const sage_attention* s, const WsView& w, const sage_tensor* q, const sage_tensor* k,
-                         const sage_tensor* v, const sage_options* opts, Geom* geom) {
+                         const sage_tensor* v, const sage_options* opts, Geom* geom, const QkvDev* qa) {
     const sage_plan& plan = w.plan;
     const uint64_t d = s->head_dim;
     const struct {
@@ -513,7 +513,8 @@ sage_status prepare_view(const sage_attention* s, const WsView& w, const sage_te
 
     PrologueBufs bufs{w.q8, w.q_scale, w.k8, w.k_scale, w.v8, w.stats, w.part, w.kbias};
     hipError_t e = launch_prologue((int)d, static_cast<const uint16_t*>(q->data), static_cast<const uint16_t*>(k->data),
-                                   static_cast<const uint16_t*>(v->data), opts->qk_norm_params, bufs, g, s->stream);
+                                   static_cast<const uint16_t*>(v->data), opts->qk_norm_params, bufs, g, qa,
+                                   s->stream);
     if (e != hipSuccess) return hip_fail(e, "launch sage prologue");
     *geom = g;
     return SAGE_OK;
@@ -551,7 +552,7 @@ sage_status sage_prepare(const sage_attention* s, sage_workspace* ws, const sage
         return fail(SAGE_ERR_INVALID, "workspace was made for head dim %llu, kernels are %llu", (u64)ws->head_dim,
                     (u64)s->head_dim);
     sage::Geom g;
-    sage_status r = sage::prepare_view(s, view_of(ws), q, k, v, opts, &g);
+    sage_status r = sage::prepare_view(s, view_of(ws), q, k, v, opts, &g, nullptr);
     if (r != SAGE_OK) return r;
     ws->geom = g;
     ws->prepared = true;
@@ -571,6 +572,223 @@ sage_status sage_attend(const sage_attention* s, const sage_workspace* ws, const
 sage_status sage_forward(const sage_attention* s, sage_workspace* ws, const sage_tensor* q, const sage_tensor* k,
                          const sage_tensor* v, const sage_tensor_mut* out, const sage_options* opts) {
     sage_status r = sage_prepare(s, ws, q, k, v, opts);
+    if (r != SAGE_OK) return r;
+    return sage_attend(s, ws, out);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- QKV prologue
+namespace {
+
+// Ptrs::input / Ptrs::output (lib.rs:247-287): "<what>: buffer holds N elements, needs M".
+bool holds(uint64_t have, uint64_t need, const char* what, sage_status* st) {
+    if (have < need) {
+        *st = fail(SAGE_ERR_INVALID, "%s: buffer holds %llu elements, needs %llu", what, (u64)have, (u64)need);
+        return false;
+    }
+    return true;
+}
+
+// check_aligned (norm.rs:361-366), for `bytes`-byte alignment.
+bool aligned(const void* p, uintptr_t bytes, sage_status* st) {
+    if (reinterpret_cast<uintptr_t>(p) % bytes) {
+        *st = fail(SAGE_ERR_INVALID, "device pointer %#llx is not %u-byte aligned",
+                   (u64) reinterpret_cast<uintptr_t>(p), (unsigned)bytes);
+        return false;
+    }
+    return true;
+}
+
+// QkvPrologue::run's checks (qkv.rs:226-278) for batch x tokens tokens of
+// heads / kv_heads heads of dimension d, in the reference's order, and the
+// kernels' options. *bs receives the batch stride of y.
+sage_status qkv_setup(uint64_t batch, uint64_t tokens, uint64_t heads, uint64_t kv, uint64_t d, const sage_qkv_in* in,
+                      const sage_qkv_norm* norm, const sage_qkv_rope* rope, sage::QkvDev* qa, uint64_t* bs) {
+    sage_status st = SAGE_OK;
+    const uint64_t width = (heads + 2 * kv) * d;
+    const uint64_t stride = in->batch_stride ? in->batch_stride : tokens * in->ld;
+    uint64_t a, b2, need;
+    if (stride % 8)
+        return fail(SAGE_ERR_INVALID, "qkv: batch stride %llu must be a multiple of 8", (u64)stride);
+    if (__builtin_mul_overflow(batch - 1, stride, &a) || __builtin_mul_overflow(tokens - 1, in->ld, &b2) ||
+        __builtin_add_overflow(a, b2, &need) || __builtin_add_overflow(need, width, &need))
+        return fail(SAGE_ERR_INVALID, "qkv y: buffer holds %llu elements, needs more than 2^64", (u64)in->y_len);
+    if (!holds(in->y_len, need, "qkv y", &st)) return st;
+    if (in->tok && !holds(in->tok_len, batch * tokens, "qkv tok scales", &st)) return st;
+    if (in->chan && !holds(in->chan_len, width, "qkv channel scales", &st)) return st;
+    if (in->bias && !holds(in->bias_len, width, "qkv bias", &st)) return st;
+    *qa = sage::QkvDev{};
+    qa->tok = in->tok;
+    qa->chan = in->chan;
+    qa->bias = in->bias;
+    if (norm) {
+        if (norm->kind != SAGE_QKV_LAYER_NORM && norm->kind != SAGE_QKV_RMS_NORM)
+            return fail(SAGE_ERR_INVALID, "qkv: unknown QK-norm kind %d", norm->kind);
+        if (!norm->q_weight || !holds(norm->len, d, "q norm weight", &st)) return norm->q_weight ? st :
+            fail(SAGE_ERR_INVALID, "q norm weight: buffer holds 0 elements, needs %llu", (u64)d);
+        if (!norm->k_weight || !holds(norm->len, d, "k norm weight", &st)) return norm->k_weight ? st :
+            fail(SAGE_ERR_INVALID, "k norm weight: buffer holds 0 elements, needs %llu", (u64)d);
+        if (norm->kind == SAGE_QKV_LAYER_NORM) {
+            if (!norm->q_bias || !norm->k_bias)
+                return fail(SAGE_ERR_INVALID, "qkv: LayerNorm QK-norm needs q and k biases");
+            if (!holds(norm->len, d, "q norm bias", &st) || !holds(norm->len, d, "k norm bias", &st)) return st;
+        }
+        const void* ps[4] = {norm->q_weight, norm->q_bias, norm->k_weight, norm->k_bias};
+        for (const void* p : ps)
+            if (p && !aligned(p, 16, &st)) return st;
+        qa->norm = norm->kind;
+        qa->nw[0] = norm->q_weight;
+        qa->nw[1] = norm->q_bias;
+        qa->nw[2] = norm->k_weight;
+        qa->nw[3] = norm->k_bias;
+        qa->eps = norm->eps;
+    }
+    if (rope) {
+        if (rope->frame_len == 0) return fail(SAGE_ERR_INVALID, "qkv: RoPE frame length is 0");
+        if (rope->layout != SAGE_ROPE_VGGT && rope->layout != SAGE_ROPE_DINOV3)
+            return fail(SAGE_ERR_INVALID, "qkv: unknown RoPE layout %d", rope->layout);
+        if (rope->frame_len > 0x7fffffffull)
+            return fail(SAGE_ERR_INVALID, "frame_len = %llu does not fit in i32", (u64)rope->frame_len);
+        if (!rope->table || !holds(rope->table_len, rope->frame_len * d, "RoPE table", &st))
+            return rope->table ? st
+                               : fail(SAGE_ERR_INVALID, "RoPE table: buffer holds 0 elements, needs %llu",
+                                      (u64)(rope->frame_len * d));
+        if (!aligned(rope->table, 16, &st)) return st;
+        qa->rope = rope->table;
+        qa->rope_half = (int)(rope->layout == SAGE_ROPE_VGGT ? d / 4 : d / 2);
+        qa->frame_len = (int)rope->frame_len;
+    }
+    if (!aligned(in->y, 16, &st) || (in->chan && !aligned(in->chan, 16, &st)) ||
+        (in->bias && !aligned(in->bias, 16, &st)) || (in->tok && !aligned(in->tok, 4, &st)))
+        return st;
+    *bs = stride;
+    return SAGE_OK;
+}
+
+bool qkv_ld_ok(const sage_qkv_in* in, uint64_t width, sage_status* st) {
+    if (in->ld < width || in->ld % 8) {
+        *st = fail(SAGE_ERR_INVALID, "qkv: ld %llu must be a multiple of 8 and at least %llu", (u64)in->ld, (u64)width);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+sage_status sage_rope_table(int32_t layout, uint64_t head_dim, uint64_t grid_h, uint64_t grid_w, uint64_t special,
+                            double base, float* out, uint64_t out_len) {
+    if (!out) return fail(SAGE_ERR_INVALID, "null argument");
+    if (layout != SAGE_ROPE_VGGT && layout != SAGE_ROPE_DINOV3)
+        return fail(SAGE_ERR_INVALID, "qkv: unknown RoPE layout %d", layout);
+    if (head_dim != 64 && head_dim != 128)
+        return fail(SAGE_ERR_INVALID, "sage attention supports head dim 64 or 128, got %llu", (u64)head_dim);
+    const uint64_t frame_len = special + grid_h * grid_w, pairs = head_dim / 2, axis = pairs / 2;
+    sage_status st = SAGE_OK;
+    if (!holds(out_len, frame_len * pairs * 2, "RoPE table", &st)) return st;
+    const double pi = 3.14159265358979323846;
+    for (uint64_t t = 0; t < frame_len; t++)
+        for (uint64_t p = 0; p < pairs; p++) {
+            double a = 0.0;
+            if (t >= special) {
+                const uint64_t y = (t - special) / grid_w, x = (t - special) % grid_w;
+                if (layout == SAGE_ROPE_VGGT) {
+                    const double pos = (double)(p < axis ? y + 1 : x + 1);
+                    a = pos * std::pow(base, -(double)(p % axis) / (double)axis);
+                } else {
+                    const double coord = p < axis ? ((double)y + 0.5) / (double)grid_h * 2.0 - 1.0
+                                                  : ((double)x + 0.5) / (double)grid_w * 2.0 - 1.0;
+                    a = 2.0 * pi * coord / std::pow(base, (double)(p % axis) / (double)axis);
+                }
+            }
+            out[(t * pairs + p) * 2] = (float)std::cos(a);
+            out[(t * pairs + p) * 2 + 1] = (float)std::sin(a);
+        }
+    return ok();
+}
+
+sage_status sage_qkv_prologue(const sage_attention* s, const sage_shape* shape, const sage_qkv_in* in,
+                              const sage_qkv_norm* norm, const sage_qkv_rope* rope, const sage_tensor_mut* q,
+                              const sage_tensor_mut* k, const sage_tensor_mut* v) {
+    if (!s || !shape || !in || !q || !k || !v) return fail(SAGE_ERR_INVALID, "null argument");
+    const uint64_t d = s->head_dim, heads = shape->heads, kv = shape->kv_heads ? shape->kv_heads : shape->heads;
+    sage_status st = SAGE_OK;
+    if (!qkv_ld_ok(in, (heads + 2 * kv) * d, &st)) return st;
+    if (shape->tokens == 0 || heads == 0 || shape->batch == 0) return ok();
+    if (heads % kv)
+        return fail(SAGE_ERR_INVALID, "%llu query heads are not a multiple of %llu KV heads", (u64)heads, (u64)kv);
+    // The kernel's grid takes the part-head slots in y and the batch in z.
+    if (shape->tokens > 0x7fffffffull || shape->batch > 65535 || heads + 2 * kv > 65535)
+        return fail(SAGE_ERR_INVALID, "qkv: %llu batch items of %llu part-head slots exceed the launch grid",
+                    (u64)shape->batch, (u64)(heads + 2 * kv));
+    sage::QkvDev qa;
+    uint64_t bs = 0;
+    st = qkv_setup(shape->batch, shape->tokens, heads, kv, d, in, norm, rope, &qa, &bs);
+    if (st != SAGE_OK) return st;
+    const sage_tensor_mut* outs[3] = {q, k, v};
+    const char* names[3] = {"qkv q", "qkv k", "qkv v"};
+    sage::QkvOutDev o{};
+    for (int i = 0; i < 3; i++) {
+        const sage_tensor_mut* t = outs[i];
+        st = sage_strides_check(&t->strides, names[i]);
+        if (st != SAGE_OK) return st;
+        const uint64_t need = sage_strides_extent(&t->strides, shape->batch, shape->tokens, i ? kv : heads, d);
+        if (!holds(t->len, need, names[i], &st) || !aligned(t->data, 16, &st)) return st;
+        const bool f16_ok = i == 2;
+        if (t->dtype != SAGE_BF16 && !(f16_ok && t->dtype == SAGE_F16))
+            return fail(SAGE_ERR_INVALID, "%s must be bf16%s", names[i], f16_ok ? " or fp16" : "");
+        o.p[i] = static_cast<uint16_t*>(t->data);
+        o.sb[i] = (long long)t->strides.batch;
+        o.st[i] = (long long)t->strides.token;
+        o.sh[i] = (long long)t->strides.head;
+    }
+    o.v_f16 = v->dtype == SAGE_F16;
+    sage::Geom g{};
+    g.batch = (int)shape->batch;
+    g.heads = (int)heads;
+    g.kv_heads = (int)kv;
+    g.tokens = (int)shape->tokens;
+    g.q_sb = (long long)bs;
+    g.q_st = (long long)in->ld;
+    hipError_t e = sage::launch_qkv((int)d, static_cast<const uint16_t*>(in->y), o, g, qa, s->stream);
+    if (e != hipSuccess) return hip_fail(e, "qkv_prologue");
+    return ok();
+}
+
+sage_status sage_prepare_qkv(const sage_attention* s, sage_workspace* ws, const sage_qkv_in* in,
+                             const sage_qkv_norm* norm, const sage_qkv_rope* rope, const sage_options* opts) {
+    if (!s || !ws || !in || !opts) return fail(SAGE_ERR_INVALID, "null argument");
+    if (ws->head_dim != s->head_dim)
+        return fail(SAGE_ERR_INVALID, "workspace was made for head dim %llu, kernels are %llu", (u64)ws->head_dim,
+                    (u64)s->head_dim);
+    const sage_shape& sh = ws->plan.shape;
+    const uint64_t d = s->head_dim, heads = sh.heads, kv = sh.kv_heads;
+    sage_status st = SAGE_OK;
+    if (!qkv_ld_ok(in, (heads + 2 * kv) * d, &st)) return st;
+    sage::QkvDev qa;
+    uint64_t bs = 0;
+    st = qkv_setup(sh.batch, sh.tokens, heads, kv, d, in, norm, rope, &qa, &bs);
+    if (st != SAGE_OK) return st;
+    // Q, K and V as views into the projection: q | k | v along the channels.
+    const uint16_t* y = static_cast<const uint16_t*>(in->y);
+    const sage_strides str{bs, in->ld, d};
+    const sage_tensor q{y, in->y_len, str, SAGE_BF16};
+    const sage_tensor k{y + heads * d, in->y_len - heads * d, str, SAGE_BF16};
+    const sage_tensor v{y + (heads + kv) * d, in->y_len - (heads + kv) * d, str, SAGE_BF16};
+    sage::Geom g;
+    st = sage::prepare_view(s, view_of(ws), &q, &k, &v, opts, &g, &qa);
+    if (st != SAGE_OK) return st;
+    ws->geom = g;
+    ws->prepared = true;
+    return ok();
+}
+
+sage_status sage_forward_qkv(const sage_attention* s, sage_workspace* ws, const sage_qkv_in* in,
+                             const sage_qkv_norm* norm, const sage_qkv_rope* rope, const sage_tensor_mut* out,
+                             const sage_options* opts) {
+    sage_status r = sage_prepare_qkv(s, ws, in, norm, rope, opts);
     if (r != SAGE_OK) return r;
     return sage_attend(s, ws, out);
 }

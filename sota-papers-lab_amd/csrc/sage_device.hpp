@@ -138,6 +138,170 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
 }
 
+// The QKV prologue's options (the reference's QkvArgs, qkv.cu:9-31): the
+// fused projection y holds, per token, q | k | v of heads * D, kv_heads * D
+// and kv_heads * D channels; null pointers switch an option off.
+struct QkvDev {
+    const float* tok;      // [batch * tokens] per-token scales
+    const float* chan;     // [(heads + 2 kv_heads) * D] per-channel scales
+    const uint16_t* bias;  // bf16 [(heads + 2 kv_heads) * D]
+    const float* nw[4];    // [D] each: q weight, q bias, k weight, k bias (biases: LayerNorm)
+    const float* rope;     // [frame_len][D / 2][2]: cos, sin of each rotation pair
+    int norm;              // 0 none, 1 LayerNorm, 2 RMSNorm
+    int rope_half;         // channels between the two of a rotation pair
+    int frame_len;         // rope row of token t: t % frame_len
+    float eps;
+};
+
+// The QKV prologue (qkv.cu:50-120) on one (token, part, head) row whose D
+// channels lie on D/8 consecutive lanes, 8 a lane (ch = the lane's chunk;
+// every lane of the wave takes part, rows past the sequence on zeros). part
+// is 0 (q), 1 (k) or 2 (v). The arithmetic, in fp32:
+//   x *= tok[b, t]; x *= chan[c]; x += bias[c] (each rounded);
+//   QK-norm (q, k): lane sums meet in an xor butterfly over 1 .. D/16,
+//   mean = s * (1/D) (0 for RMSNorm), fused square deviations, r = 1 / sqrt(
+//   fmaf(ss, 1/D, eps)) with the square root and the divide correctly
+//   rounded (the reference's rsqrtf does not state its rounding), x =
+//   fmaf((x - mean) * r, w, LayerNorm ? b : 0);
+//   RoPE (q, k): the partner channel d ^ half sits on lane ^ (half / 8);
+//   x = fmaf(x, cos, +-(partner * sin)), minus when d & half == 0.
+// Loads are split from the arithmetic: QkvLane holds what depends on the
+// lane's channels only (loaded once per part and head), QkvTok what depends
+// on the token (its scale and the lane's 8 rotation pairs, 64 contiguous
+// bytes of the table row since a lane's 8 channels rotate 8 consecutive
+// pairs).
+// Sum over the CH lanes of a row group (CH = 2, 4, 8 or 16 consecutive lanes,
+// aligned), equal to the xor butterfly v += shfl_xor(v, 1), (v, 2), (v, 4),
+// (v, 8) bit for bit, on DPP instead of the LDS crossbar: after each step all
+// lanes of the quad (then of the half row) hold the same value, so pairing
+// the quads by row_half_mirror and the half rows by row_mirror adds the same
+// two values that xor 4 and xor 8 would.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CH>
+__device__ __forceinline__ float row_sum(float v) {
+    v += dpp<0xB1>(v);                    // quad_perm [1, 0, 3, 2]: lane ^ 1
+    if (CH > 2) v += dpp<0x4E>(v);        // quad_perm [2, 3, 0, 1]: lane ^ 2
+    if (CH > 4) v += dpp<0x141>(v);       // row_half_mirror: the other quad of the 8
+    if (CH > 8) v += dpp<0x140>(v);       // row_mirror: the other 8 of the 16
+    return v;
+}
+
+struct QkvLane {
+    float chan[8], bias[8], w[8], nb[8];
+};
+struct QkvTok {
+    float t;
+    float4 cs[4];  // (cos, sin) of the lane's pairs 2i (x, y) and 2i + 1 (z, w)
+};
+
+__device__ __forceinline__ int qkv_slot(const Geom& g, int part, int h) {
+    return part == 0 ? h : (part == 1 ? g.heads + h : g.heads + g.kv_heads + h);
+}
+
+template <int D>
+__device__ __forceinline__ void qkv_lane(QkvLane& L, const QkvDev& a, const Geom& g, int part, int h, int ch) {
+    const int c0 = qkv_slot(g, part, h) * D + ch * 8;
+    auto load8 = [](const float* p, float* o) {
+        const float4 u = *reinterpret_cast<const float4*>(p), v = *reinterpret_cast<const float4*>(p + 4);
+        o[0] = u.x, o[1] = u.y, o[2] = u.z, o[3] = u.w, o[4] = v.x, o[5] = v.y, o[6] = v.z, o[7] = v.w;
+    };
+    if (a.chan) load8(a.chan + c0, L.chan);
+    if (a.bias) unpack8(*reinterpret_cast<const uint4*>(a.bias + c0), L.bias, false);
+    if (a.norm && part < 2) {
+        load8(a.nw[2 * part] + ch * 8, L.w);
+        // The bias pointer is valid either way (the weight's under RMSNorm,
+        // where the value is selected away).
+        load8((a.norm == 1 ? a.nw[2 * part + 1] : a.nw[2 * part]) + ch * 8, L.nb);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void qkv_tok(QkvTok& T, const QkvDev& a, const Geom& g, int part, int b, int tok, int ch) {
+    if (a.tok) T.t = a.tok[(long long)b * g.tokens + min(tok, g.tokens - 1)];
+    if (a.rope && part < 2) {
+        const int half = a.rope_half, d0 = ch * 8;
+        const int pair0 = (d0 / (2 * half)) * half + d0 % half;
+        const float4* row = reinterpret_cast<const float4*>(a.rope + (long long)(tok % a.frame_len) * D + 2 * pair0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) T.cs[i] = row[i];
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void qkv_apply(float* x, const QkvDev& a, const QkvLane& L, const QkvTok& T, int part,
+                                          int ch) {
+    constexpr int CH = D / 8;
+    if (a.tok) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = x[e] * T.t;
+    }
+    if (a.chan) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = x[e] * L.chan[e];
+    }
+    if (a.bias) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = x[e] + L.bias[e];
+    }
+    // The norm's and the rotation's shuffles run on every lane (part need not
+    // be uniform across a wave); only the updates depend on the part.
+    if (a.norm) {
+        // LayerNorm and RMSNorm differ by selects only, with no branch between
+        // them: the row sum is formed either way. (A version with the
+        // LayerNorm mean behind its own branch was compiled by ROCm 7.2's
+        // hipcc into code that left one channel of each K row undefined under
+        // RMSNorm.)
+        const bool layer = a.norm == 1;
+        float sum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) sum += x[e];
+        sum = row_sum<CH>(sum);
+        const float mean = layer ? sum * (1.0f / D) : 0.0f;
+        float s2 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float d = x[e] - mean;
+            s2 = __builtin_fmaf(d, d, s2);
+        }
+        s2 = row_sum<CH>(s2);
+        if (part < 2) {
+            const float r = 1.0f / sqrtf(__builtin_fmaf(s2, 1.0f / D, a.eps));
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = __builtin_fmaf((x[e] - mean) * r, L.w[e], layer ? L.nb[e] : 0.0f);
+        }
+    }
+    if (a.rope) {
+        const int half = a.rope_half, xo = half >> 3;
+        float p[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) p[e] = __shfl_xor(x[e], xo, 64);
+        if (part < 2) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float4 q = T.cs[e >> 1];
+                const float c = (e & 1) ? q.z : q.x, sn = (e & 1) ? q.w : q.y;
+                const float ps = p[e] * sn;
+                x[e] = __builtin_fmaf(x[e], c, ((ch * 8 + e) & half) ? ps : -ps);
+            }
+        }
+    }
+}
+
+// Destinations of the standalone QKV prologue: 16-bit [batch][token][head][D]
+// views of Q, K and V (p[0..2], element strides sb, st, sh), V in fp16 when
+// v_f16 (the reference's VFormat::F16), else bf16 like Q and K.
+struct QkvOutDev {
+    uint16_t* p[3];
+    long long sb[3], st[3], sh[3];
+    int v_f16;
+};
+
+// x rounded to the nearest bf16 (ties to even), as a float.
+__device__ __forceinline__ float round_bf16(float x) { return __uint_as_float(pack_bf16x2(x, 0.f) << 16); }
+
 // Byte position of key k (0..63) of a 64-key block inside each channel row of
 // the V tile. The 32x32 INT8 MFMA leaves key 32t + 8j + 4g + r of a column
 // in lane-half g, accumulator 4j + r of sub-tile t; packed four to a register

@@ -17,6 +17,8 @@ struct sage_attention {
 namespace sage {
 
 struct Geom;
+struct QkvDev;
+struct QkvOutDev;
 
 // Device buffers the prologue writes (a workspace's view).
 struct PrologueBufs {
@@ -44,8 +46,15 @@ struct AttendBufs {
 
 // ln: [4][head_dim] QK LayerNorm parameters (q weight, q bias, k weight,
 // k bias), read only under F_LN_Q / F_LN_K; may be null otherwise.
+// qa: the QKV prologue's options when q, k and v point into a fused QKV
+// projection (sage_prepare_qkv), or null for plain 16-bit inputs.
 hipError_t launch_prologue(int head_dim, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ln,
-                           const PrologueBufs& w, const Geom& g, hipStream_t s);
+                           const PrologueBufs& w, const Geom& g, const QkvDev* qa, hipStream_t s);
+
+// The reference's qkv_prologue on its own (QkvPrologue::run): the fused
+// projection y (strides g.q_sb, g.q_st) to 16-bit Q, K and V rows.
+hipError_t launch_qkv(int head_dim, const uint16_t* y, const QkvOutDev& o, const Geom& g, const QkvDev& qa,
+                      hipStream_t s);
 
 // Rows of queries one attention workgroup owns.
 constexpr int ATTN_ROWS = 128;
@@ -89,8 +98,10 @@ sage_status workspace_layout(const sage_attention* s, const sage_shape* shape, c
 // The bodies of prepare and attend on a buffer view: every check before any
 // launch, then the launches on s->stream. prepare_view returns the kernel
 // parameters attend_view needs.
+// qa: the QKV prologue's options when q, k and v are views into a fused
+// QKV projection (sage_prepare_qkv), or null.
 sage_status prepare_view(const sage_attention* s, const WsView& w, const sage_tensor* q, const sage_tensor* k,
-                         const sage_tensor* v, const sage_options* opts, Geom* geom);
+                         const sage_tensor* v, const sage_options* opts, Geom* geom, const QkvDev* qa);
 sage_status attend_view(const sage_attention* s, const WsView& w, const Geom& geom, const sage_tensor_mut* out);
 
 }  // namespace sage

@@ -94,7 +94,7 @@ extern "C" sage_status sage_forward_noalloc(const sage_attention* s, const sage_
                          static_cast<float*>(buf[6]),
                          static_cast<float*>(buf[7])};
     sage::Geom g;
-    st = sage::prepare_view(s, w, q, k, v, opts, &g);
+    st = sage::prepare_view(s, w, q, k, v, opts, &g, nullptr);
     if (st != SAGE_OK) return st;
     st = sage::attend_view(s, w, g, out);
     if (st != SAGE_OK) return st;

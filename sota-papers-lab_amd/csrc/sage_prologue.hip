@@ -2,11 +2,11 @@
 // scale per 16 rows), INT8 K (one scale per 64 keys), FP8 E4M3 V (one scale
 // per channel). Three HBM-bound launches:
 //
-//   sage_prep      grid (2 q_tiles, kv_heads, batch): per 128-token tile, one
-//                  workgroup writes the partial K sum, V sum, V min, V max of
-//                  every channel, another the INT8 Q of the `group` query
-//                  heads that share the KV head (Q and K rows LayerNormed
-//                  first under QK LayerNorm)
+//   sage_prep      grid ((1 + group) q_tiles, kv_heads, batch): per 128-token
+//                  tile, one workgroup writes the partial K sum, V sum, V min,
+//                  V max of every channel, and one per query head of the
+//                  group that shares the KV head its INT8 Q (Q and K rows
+//                  LayerNormed first under QK LayerNorm)
 //   sage_finalize  grid (kv_heads, batch): K mean, V mean, V scale, 1/V scale
 //   sage_quant_kv  grid (kblocks, kv_heads, batch): smoothed INT8 K and FP8 V,
 //                  V transposed per 64-key block into the MFMA operand order;
@@ -26,6 +26,8 @@
 // read or written exactly once goes around it (non-temporal): the Q load and
 // the q8, k8 and v8 stores. The attention kernel shares its K/V tiles through
 // L2, not through that cache.
+#include <algorithm>
+
 #include "sage_device.hpp"
 #include "sage_internal.hpp"
 
@@ -87,6 +89,18 @@ __device__ __forceinline__ void layernorm8(float* x, const float* __restrict__ w
     for (int e = 0; e < 8; e++) x[e] = __builtin_fmaf((x[e] - mean) * rstd, w[ch * 8 + e], bias[ch * 8 + e]);
 }
 
+// One row chunk of the fused QKV projection as the reference's QKV prologue
+// leaves it for the sage prologue (qkv.cu:37-133): transformed in fp32
+// (qkv_apply), then rounded to bf16 as qkv_prologue's store rounds it, so
+// the codes equal those of running that prologue and then this one.
+template <int D>
+__device__ __forceinline__ void qkv_row(float* x, const QkvDev& qa, const QkvLane& L, const QkvTok& T, int part,
+                                        int ch) {
+    qkv_apply<D>(x, qa, L, T, part, ch);
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[e] = round_bf16(x[e]);
+}
+
 // sage_quant.cu:59-160 (sg_prep), in two roles. Under QK LayerNorm (LN, the
 // F_LN_Q and F_LN_K flags together as the reference sets them) every K row is
 // normalised before the statistics read it and every Q row before its amax;
@@ -94,10 +108,10 @@ __device__ __forceinline__ void layernorm8(float* x, const float* __restrict__ w
 
 // K and V channel statistics of one 128-token tile (sage_quant.cu:73-80,
 // 97-107, 129-159): the tile's partial K sum, V sum, V min and V max.
-template <int D, bool LN>
+template <int D, bool LN, bool QKV>
 __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                            const float* __restrict__ ln, float* __restrict__ part, const Geom& g,
-                                           int tile, int hk, int b, float (*red)[4][D]) {
+                                           const QkvDev& qa, int tile, int hk, int b, float (*red)[4][D]) {
     constexpr int CH = D / 8;        // 16-byte chunks per head row
     constexpr int TPI = 256 / CH;    // tokens per iteration
     constexpr int NI = QTILE / TPI;  // iterations
@@ -112,20 +126,13 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
         vmn[e] = 3.0e38f;
         vmx[e] = -3.0e38f;
     }
-    uint4 kraw[NI], vraw[NI];
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-        const int tok = tile * QTILE + slot + i * TPI;
-        const bool ok = tok < g.tokens;
-        kraw[i] = load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, ok);
-        vraw[i] = load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, ok);
+    QkvLane lk, lv;
+    if (QKV) {
+        qkv_lane<D>(lk, qa, g, 1, hk, ch);
+        qkv_lane<D>(lv, qa, g, 2, hk, ch);
     }
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-        const int tok = tile * QTILE + slot + i * TPI;
-        float fk[8], fv[8];
-        unpack8(kraw[i], fk, f16);
-        unpack8(vraw[i], fv, f16);
+    // Row i of the thread (token tok) into the running sums, in i order.
+    auto accumulate = [&](int tok, float* fk, float* fv) __attribute__((always_inline)) {
         if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
         if (tok < g.tokens) {
 #pragma unroll
@@ -135,6 +142,41 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
                 vmn[e] = fminf(vmn[e], fv[e]);
                 vmx[e] = fmaxf(vmx[e], fv[e]);
             }
+        }
+    };
+    if constexpr (QKV) {
+        // Rows of the fused projection carry their QKV-prologue arithmetic;
+        // two at a time keeps the registers of more waves (other waves hide
+        // the loads' latency).
+#pragma unroll 2
+        for (int i = 0; i < NI; i++) {
+            const int tok = tile * QTILE + slot + i * TPI;
+            const bool ok = tok < g.tokens;
+            float fk[8], fv[8];
+            QkvTok tt;
+            qkv_tok<D>(tt, qa, g, 1, b, tok, ch);
+            unpack8(load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, ok), fk, false);
+            unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, ok), fv, false);
+            qkv_row<D>(fk, qa, lk, tt, 1, ch);
+            qkv_row<D>(fv, qa, lv, tt, 2, ch);
+            accumulate(tok, fk, fv);
+        }
+    } else {
+        uint4 kraw[NI], vraw[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int tok = tile * QTILE + slot + i * TPI;
+            const bool ok = tok < g.tokens;
+            kraw[i] = load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, ok);
+            vraw[i] = load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, ok);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int tok = tile * QTILE + slot + i * TPI;
+            float fk[8], fv[8];
+            unpack8(kraw[i], fk, f16);
+            unpack8(vraw[i], fv, f16);
+            accumulate(tok, fk, fv);
         }
     }
     // Lanes of one 32-lane half that hold the same channels, then the halves
@@ -171,22 +213,24 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
     }
 }
 
-// INT8 Q of one 128-token tile of every query head that reads KV head hk
-// (sage_quant.cu:85-127).
-template <int D, bool LN>
+// INT8 Q of one 128-token tile of query head gi of the `group` heads that
+// read KV head hk (sage_quant.cu:85-127).
+template <int D, bool LN, bool QKV>
 __device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const float* __restrict__ ln,
                                         int8_t* __restrict__ q8, float* __restrict__ q_scale, const Geom& g,
-                                        int tile, int hk, int b, unsigned* gmax) {
+                                        const QkvDev& qa, int tile, int hk, int gi, int b, unsigned* gmax) {
     constexpr int CH = D / 8;
     constexpr int TPI = 256 / CH;
     constexpr int NI = QTILE / TPI;
     const int tid = threadIdx.x, ch = tid % CH, slot = tid / CH;
     const bool f16 = g.flags & F_IN_F16;
-    for (int gi = 0; gi < g.group; gi++) {
+    {
         const int h = hk * g.group + gi;
         const long long bh = (long long)b * g.heads + h;
         if (tid < QTILE / QGROUP) gmax[tid] = 0u;
         __syncthreads();
+        QkvLane lq;
+        if (QKV) qkv_lane<D>(lq, qa, g, 0, h, ch);
         uint4 qraw[NI];
 #pragma unroll
         for (int i = 0; i < NI; i++) {
@@ -197,12 +241,16 @@ __device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const fl
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             unpack8(qraw[i], qv[i], f16);
-            if (LN) {
-                layernorm8<D>(qv[i], ln, ln + D, ch, g.ln_eps);
-                if (tile * QTILE + slot + i * TPI >= g.tokens) {
+            const int tok = tile * QTILE + slot + i * TPI;
+            if (QKV) {
+                QkvTok tt;
+                qkv_tok<D>(tt, qa, g, 0, b, tok, ch);
+                qkv_row<D>(qv[i], qa, lq, tt, 0, ch);
+            }
+            if (LN) layernorm8<D>(qv[i], ln, ln + D, ch, g.ln_eps);
+            if ((LN || QKV) && tok >= g.tokens) {
 #pragma unroll
-                    for (int e = 0; e < 8; e++) qv[i][e] = 0.f;  // padding rows stay zero
-                }
+                for (int e = 0; e < 8; e++) qv[i][e] = 0.f;  // padding rows stay zero
             }
             float amax = 0.f;
 #pragma unroll
@@ -230,21 +278,24 @@ __device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const fl
     }
 }
 
-// Two workgroups a tile: even blockIdx.x the K/V statistics, odd the INT8 Q.
-// The reference's one thread block does both in turn; split, the two streams
-// of loads overlap across workgroups.
-template <int D, bool LN>
+// 1 + group workgroups a tile: the first the K/V statistics, each other the
+// INT8 Q of one query head of the KV head's group. The reference's one
+// thread block does all of it in turn; split, the streams of loads overlap
+// across workgroups, and grouped-query plans spread their Q heads over
+// workgroups instead of walking them in one.
+template <int D, bool LN, bool QKV>
 __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                  const uint16_t* __restrict__ v, const float* __restrict__ ln,
                                                  int8_t* __restrict__ q8, float* __restrict__ q_scale,
-                                                 float* __restrict__ part, Geom g) {
+                                                 float* __restrict__ part, Geom g, QkvDev qa) {
     __shared__ unsigned gmax[QTILE / QGROUP];
     __shared__ float red[8][4][D];
-    const int tile = (int)blockIdx.x >> 1, hk = blockIdx.y, b = blockIdx.z;
-    if (blockIdx.x & 1)
-        tile_q8<D, LN>(q, ln, q8, q_scale, g, tile, hk, b, gmax);
+    const int roles = 1 + g.group, tile = (int)blockIdx.x / roles, role = (int)blockIdx.x % roles;
+    const int hk = blockIdx.y, b = blockIdx.z;
+    if (role)
+        tile_q8<D, LN, QKV>(q, ln, q8, q_scale, g, qa, tile, hk, role - 1, b, gmax);
     else
-        tile_stats<D, LN>(k, v, ln, part, g, tile, hk, b, red);
+        tile_stats<D, LN, QKV>(k, v, ln, part, g, qa, tile, hk, b, red);
 }
 
 // sage_quant.cu:163-206 (sg_finalize): even and odd tiles folded separately.
@@ -325,12 +376,12 @@ __device__ __forceinline__ void put_v(uint8_t* vt, int ch, int kl, const float* 
 // `sum * rc - mean`, equal to the dense (k + 0) - mean when n = 1.
 // Under QK LayerNorm (LN) each K row (each member, when merging) is
 // normalised before it is summed (sage_quant.cu:271).
-template <int D, bool LN>
+template <int D, bool LN, bool QKV>
 __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                      const float* __restrict__ ln,
                                                      const float* __restrict__ stats, int8_t* __restrict__ k8,
                                                      float* __restrict__ k_scale, uint8_t* __restrict__ v8,
-                                                     float* __restrict__ kbias, Geom g) {
+                                                     float* __restrict__ kbias, Geom g, QkvDev qa) {
     constexpr int CH = D / 8;
     constexpr int TPI = 256 / CH;
     constexpr int NI = KBLOCK / TPI;
@@ -351,6 +402,11 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
         mv[e] = st[D + ch * 8 + e];
         iv[e] = st[3 * D + ch * 8 + e];
     }
+    QkvLane lk, lv;
+    if (QKV) {
+        qkv_lane<D>(lk, qa, g, 1, hk, ch);
+        qkv_lane<D>(lv, qa, g, 2, hk, ch);
+    }
     float kv[NI][8];
     float amax = 0.f;
     if (g.merge == 1) {
@@ -370,6 +426,12 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
             float fk[8], fv[8];
             unpack8(kraw[i], fk, f16);
             unpack8(vraw[i], fv, f16);
+            if (QKV) {
+                QkvTok tt;
+                qkv_tok<D>(tt, qa, g, 1, b, blk * KBLOCK + kl, ch);
+                qkv_row<D>(fk, qa, lk, tt, 1, ch);
+                qkv_row<D>(fv, qa, lv, tt, 2, ch);
+            }
             if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
             float vq[8];
 #pragma unroll
@@ -400,6 +462,12 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
                 float fk[8], fv[8];
                 unpack8(load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, mok), fk, f16);
                 unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, mok), fv, f16);
+                if (QKV) {
+                    QkvTok tt;
+                    qkv_tok<D>(tt, qa, g, 1, b, tok, ch);
+                    qkv_row<D>(fk, qa, lk, tt, 1, ch);
+                    qkv_row<D>(fv, qa, lv, tt, 2, ch);
+                }
                 if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
                 if (mok) {
 #pragma unroll
@@ -456,27 +524,95 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
     }
 }
 
-template <int D, bool LN>
+// qkv.cu:37-133 (qkv_prologue) on its own: every (batch, token, part, head)
+// row of the fused projection stored as 16-bit rows of Q, K and V (V in fp16
+// when asked, from the fp32 value as the reference's cvt.rn.f16x2 takes it).
+// A workgroup owns one part-head slot r (blockIdx.y; slot r starts at channel
+// r * D of a projection row) of one batch item (blockIdx.z) and walks its
+// tokens 256 / (D/8) at a time, D/8 lanes a token, so the lane's channel
+// scales, bias and norm weights are loaded once. The projection's strides
+// are g.q_sb (batch) and g.q_st (token). Tokens past the end compute on
+// zeros, so every lane takes part in the shuffles, and store nothing.
+template <int D>
+__global__ __launch_bounds__(256) void sage_qkv(const uint16_t* __restrict__ y, QkvOutDev o, Geom g, QkvDev qa) {
+    constexpr int CH = D / 8, RPB = 256 / CH;
+    const int ch = threadIdx.x % CH, r = blockIdx.y, b = blockIdx.z;
+    const int part = r < g.heads ? 0 : (r < g.heads + g.kv_heads ? 1 : 2);
+    const int h = part == 0 ? r : (part == 1 ? r - g.heads : r - g.heads - g.kv_heads);
+    QkvLane lane;
+    qkv_lane<D>(lane, qa, g, part, h, ch);
+    const uint16_t* yb = y + b * g.q_sb + (long long)r * D + ch * 8;
+    uint16_t* ob = o.p[part] + b * o.sb[part] + h * o.sh[part] + ch * 8;
+    const long long ost = o.st[part];
+    const bool f16 = part == 2 && o.v_f16;
+    for (int t0 = blockIdx.x * RPB; t0 < g.tokens; t0 += gridDim.x * RPB) {
+        const int tok = t0 + (int)threadIdx.x / CH;
+        const bool valid = tok < g.tokens;
+        QkvTok tt;
+        qkv_tok<D>(tt, qa, g, part, b, valid ? tok : 0, ch);
+        float x[8];
+        unpack8(load16(yb + (long long)tok * g.q_st, valid), x, false);
+        qkv_apply<D>(x, qa, lane, tt, part, ch);
+        if (valid) {
+            uint4 w;
+            if (f16) {
+                w = make_uint4(pack_f16x2(x[0], x[1]), pack_f16x2(x[2], x[3]), pack_f16x2(x[4], x[5]),
+                               pack_f16x2(x[6], x[7]));
+            } else {
+                w = make_uint4(pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3]), pack_bf16x2(x[4], x[5]),
+                               pack_bf16x2(x[6], x[7]));
+            }
+            *reinterpret_cast<uint4*>(ob + (long long)tok * ost) = w;
+        }
+    }
+}
+
+hipError_t launch_qkv(int head_dim, const uint16_t* y, const QkvOutDev& o, const Geom& g, const QkvDev& qa,
+                      hipStream_t s) {
+    const int rpb = 256 / (head_dim / 8);
+    const int slots = g.heads + 2 * g.kv_heads;
+    // About 16 workgroups a CU in all; each walks its slot's tokens.
+    const long long want = std::max(1LL, (256LL * 16 + (long long)slots * g.batch - 1) / ((long long)slots * g.batch));
+    const unsigned bx = (unsigned)std::min<long long>(want, (g.tokens + rpb - 1) / rpb);
+    const dim3 grid(bx, slots, g.batch);
+    if (head_dim == 64)
+        hipLaunchKernelGGL(sage_qkv<64>, grid, dim3(256), 0, s, y, o, g, qa);
+    else
+        hipLaunchKernelGGL(sage_qkv<128>, grid, dim3(256), 0, s, y, o, g, qa);
+    return hipGetLastError();
+}
+
+template <int D, bool LN, bool QKV>
 static hipError_t launch_prologue_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ln,
-                                    const PrologueBufs& w, const Geom& g, hipStream_t s) {
-    hipLaunchKernelGGL((sage_prep<D, LN>), dim3(2 * g.q_tiles, g.kv_heads, g.batch), dim3(256), 0, s, q, k, v, ln, w.q8,
-                       w.q_scale, w.part, g);
+                                    const PrologueBufs& w, const Geom& g, const QkvDev& qa, hipStream_t s) {
+    hipLaunchKernelGGL((sage_prep<D, LN, QKV>), dim3((1 + g.group) * g.q_tiles, g.kv_heads, g.batch), dim3(256), 0, s,
+                       q, k, v, ln,
+                       w.q8, w.q_scale, w.part, g, qa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(sage_finalize<D>, dim3(g.kv_heads, g.batch), dim3(4 * D), 0, s, w.part, w.stats, g);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((sage_quant_kv<D, LN>), dim3(g.kblocks, g.kv_heads, g.batch), dim3(256), 0, s, k, v, ln, w.stats,
-                       w.k8, w.k_scale, w.v8, w.kbias, g);
+    hipLaunchKernelGGL((sage_quant_kv<D, LN, QKV>), dim3(g.kblocks, g.kv_heads, g.batch), dim3(256), 0, s, k, v, ln,
+                       w.stats, w.k8, w.k_scale, w.v8, w.kbias, g, qa);
     return hipGetLastError();
 }
 
+template <int D, bool LN>
+static hipError_t launch_prologue_q(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ln,
+                                    const PrologueBufs& w, const Geom& g, const QkvDev* qa, hipStream_t s) {
+    if (qa) return launch_prologue_d<D, LN, true>(q, k, v, ln, w, g, *qa, s);
+    return launch_prologue_d<D, LN, false>(q, k, v, ln, w, g, QkvDev{}, s);
+}
+
 hipError_t launch_prologue(int head_dim, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ln,
-                           const PrologueBufs& w, const Geom& g, hipStream_t s) {
+                           const PrologueBufs& w, const Geom& g, const QkvDev* qa, hipStream_t s) {
     const bool norm = (g.flags & (F_LN_Q | F_LN_K)) == (F_LN_Q | F_LN_K);
     if (head_dim == 64)
-        return norm ? launch_prologue_d<64, true>(q, k, v, ln, w, g, s) : launch_prologue_d<64, false>(q, k, v, ln, w, g, s);
-    return norm ? launch_prologue_d<128, true>(q, k, v, ln, w, g, s) : launch_prologue_d<128, false>(q, k, v, ln, w, g, s);
+        return norm ? launch_prologue_q<64, true>(q, k, v, ln, w, g, qa, s)
+                    : launch_prologue_q<64, false>(q, k, v, ln, w, g, qa, s);
+    return norm ? launch_prologue_q<128, true>(q, k, v, ln, w, g, qa, s)
+                : launch_prologue_q<128, false>(q, k, v, ln, w, g, qa, s);
 }
 
 }  // namespace sage

@@ -489,6 +489,18 @@ class SageAttention:
         self.prepare(ws, q, k, v, opts)
         self.attend(ws, out)
 
+    def prepare_qkv(self, ws: Workspace, input, norm=None, rope=None, opts: Optional[Options] = None) -> None:
+        """prepare fed straight from the fused QKV projection (spl_sage.qkv)."""
+        from . import qkv
+
+        qkv.prepare_qkv(self, ws, input, norm, rope, opts)
+
+    def forward_qkv(self, ws: Workspace, input, out: TensorMut, norm=None, rope=None,
+                    opts: Optional[Options] = None) -> None:
+        from . import qkv
+
+        qkv.forward_qkv(self, ws, input, out, norm, rope, opts)
+
     def forward_noalloc(self, shape: Shape, q: Tensor, k: Tensor, v: Tensor, out: TensorMut,
                         opts: Optional[Options] = None, merge: KvMerge = KvMerge.Dense) -> None:
         """forward without a workspace (sage_forward_noalloc): the buffers come

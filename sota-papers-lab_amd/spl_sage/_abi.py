@@ -80,6 +80,25 @@ class sage_ws_buffers(C.Structure):
     ]
 
 
+class sage_qkv_in(C.Structure):
+    _fields_ = [
+        ("y", C.c_void_p), ("y_len", u64), ("ld", u64), ("batch_stride", u64),
+        ("tok", C.c_void_p), ("tok_len", u64), ("chan", C.c_void_p), ("chan_len", u64),
+        ("bias", C.c_void_p), ("bias_len", u64),
+    ]
+
+
+class sage_qkv_norm(C.Structure):
+    _fields_ = [
+        ("kind", i32), ("q_weight", C.c_void_p), ("q_bias", C.c_void_p), ("k_weight", C.c_void_p),
+        ("k_bias", C.c_void_p), ("len", u64), ("eps", C.c_float),
+    ]
+
+
+class sage_qkv_rope(C.Structure):
+    _fields_ = [("table", C.c_void_p), ("table_len", u64), ("layout", i32), ("frame_len", u64)]
+
+
 P = C.POINTER
 # name -> (restype, argtypes); every symbol include/sage_hip.h declares.
 SIGNATURES = {
@@ -113,6 +132,20 @@ SIGNATURES = {
         i32,
         [C.c_void_p, P(sage_shape), P(sage_kv_merge), P(sage_tensor), P(sage_tensor), P(sage_tensor),
          P(sage_tensor_mut), P(sage_options)],
+    ),
+    "sage_rope_table": (i32, [i32, u64, u64, u64, u64, C.c_double, C.c_void_p, u64]),
+    "sage_qkv_prologue": (
+        i32,
+        [C.c_void_p, P(sage_shape), P(sage_qkv_in), P(sage_qkv_norm), P(sage_qkv_rope), P(sage_tensor_mut),
+         P(sage_tensor_mut), P(sage_tensor_mut)],
+    ),
+    "sage_prepare_qkv": (
+        i32, [C.c_void_p, C.c_void_p, P(sage_qkv_in), P(sage_qkv_norm), P(sage_qkv_rope), P(sage_options)],
+    ),
+    "sage_forward_qkv": (
+        i32,
+        [C.c_void_p, C.c_void_p, P(sage_qkv_in), P(sage_qkv_norm), P(sage_qkv_rope), P(sage_tensor_mut),
+         P(sage_options)],
     ),
     "sage_v8_position": (i32, [i32]),
     "sage_peak": (i32, [C.c_void_p, i32, i32, P(C.c_double)]),

@@ -64,21 +64,26 @@ def run(torch, p, q, k, v, out_dtype=None, q_layout="bthd", out_layout="bthd", w
     o = from_device16(out)
     if out_layout == "bhtd":
         o = np.ascontiguousarray(o.transpose(0, 2, 1, 3))
-    pro = None
-    if want_ws:
-        plan = ws.plan()
-        get = lambda n: ws.tensor(n).cpu().numpy()
-        pro = {
-            "q8": get("q8").reshape(B, H, plan.tq_pad, D),
-            "q_scale": get("q_scale").reshape(B, H, plan.tq_pad // 16),
-            "k8": get("k8").reshape(B, HK, plan.tk_pad, D),
-            "k_scale": get("k_scale").reshape(B, HK, plan.tk_pad // 64),
-            "v8": v8_logical(get("v8"), B, HK, plan.tk_pad, D),
-            "stats": get("stats").reshape(B, HK, 4, D),
-        }
-        if p.merge > 1:
-            pro["kbias"] = get("kbias").reshape(plan.tk_pad)
-    return pro, o
+    return (read_workspace(ws, p) if want_ws else None), o
+
+
+def read_workspace(ws, p) -> dict:
+    """A prepared workspace's codes, scales and statistics in the oracle's
+    logical layouts."""
+    B, H, HK, D = p.batch, p.heads, p.hk, p.head_dim
+    plan = ws.plan()
+    get = lambda n: ws.tensor(n).cpu().numpy()
+    pro = {
+        "q8": get("q8").reshape(B, H, plan.tq_pad, D),
+        "q_scale": get("q_scale").reshape(B, H, plan.tq_pad // 16),
+        "k8": get("k8").reshape(B, HK, plan.tk_pad, D),
+        "k_scale": get("k_scale").reshape(B, HK, plan.tk_pad // 64),
+        "v8": v8_logical(get("v8"), B, HK, plan.tk_pad, D),
+        "stats": get("stats").reshape(B, HK, 4, D),
+    }
+    if p.merge > 1:
+        pro["kbias"] = get("kbias").reshape(plan.tk_pad)
+    return pro
 
 
 def assert_prologue_equal(got: dict, want: dict) -> None:

@@ -1,0 +1,183 @@
+"""The QKV prologue on the GPU (sezer-muhammed/sota-papers-lab,
+platform/spl-nn/src/qkv.rs, cuda/qkv.cu), through the C ABI:
+
+- QkvPrologue::run (sage_qkv_prologue) against the oracle's restatement of
+  the kernel's fp32 arithmetic, bit for bit (bf16 Q and K, bf16 or fp16 V),
+  on the reference test's VGGT layout (689-token frames, tests.rs:447-570)
+  and its four option sets, plus head dim 128, grouped heads, batch 2 and the
+  reference's head-major output;
+- the fused sage_prepare_qkv: the workspace's codes and scales equal the
+  oracle prologue of the oracle QKV prologue's bf16 Q, K and V bit for bit,
+  and the attention output equals the unfused GPU path (sage_qkv_prologue,
+  then prepare and attend) bit for bit, and meets the north-star gate;
+- the reference's refusals, before any launch."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import from_device16
+from sage_gpu_helpers import assert_prologue_equal, gather_rows, read_workspace, run, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+GRID_H, GRID_W, SPECIAL = 21, 32, 17
+FRAME = SPECIAL + GRID_H * GRID_W  # 689
+
+
+def _spec(O, rng, D, heads, kv, batch, tokens, norm, rope, scaled, ld_pad=8):
+    s = O.QkvSpec(batch, tokens, heads, D, kv_heads=kv)
+    s.ld = s.width + ld_pad
+    if scaled:
+        s.tok = (0.5 + rng.random(batch * tokens)).astype(np.float32)
+        s.chan = (0.5 + rng.random(s.width)).astype(np.float32)
+    s.bias = O.encode16((0.2 * rng.standard_normal(s.width)).astype(np.float32), 0)
+    if norm:
+        s.norm = norm
+        s.norm_w = np.stack([1 + 0.2 * rng.standard_normal(D), 0.1 * rng.standard_normal(D),
+                             1 + 0.2 * rng.standard_normal(D), 0.1 * rng.standard_normal(D)]).astype(np.float32)
+    if rope is not None:
+        s.rope = O.rope_table(rope, D, GRID_H, GRID_W, SPECIAL, 100.0)
+        s.rope_layout = rope
+    y = rng.standard_normal((batch, tokens, s.ld)).astype(np.float32)
+    y[..., :s.width] += 0.5 * rng.standard_normal(s.width).astype(np.float32)  # per-channel offsets
+    return s, O.encode16(y, 0)
+
+
+def _device(torch, s, y):
+    """(QkvIn, QkNorm or None, Rope or None) on the GPU."""
+    from spl_sage import qkv as Q
+
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+    f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    inp = Q.QkvIn(bf(y), s.ld, tok=None if s.tok is None else f32(s.tok), chan=None if s.chan is None else f32(s.chan),
+                  bias=None if s.bias is None else bf(s.bias), batch_stride=s.tokens * s.ld)
+    norm = None
+    if s.norm:
+        w = [f32(s.norm_w[i]) for i in range(4)]
+        norm = Q.QkNorm(Q.NormKind(s.norm), w[0], w[2], w[1], w[3], float(s.eps))
+    rope = None
+    if s.rope is not None:
+        rope = Q.Rope(f32(s.rope.reshape(-1)), Q.RopeLayout(s.rope_layout), s.rope.shape[0])
+    return inp, norm, rope
+
+
+STANDALONE = [  # (D, heads, kv, batch, frames, norm, rope, scaled, head_major)
+    (64, 16, 0, 1, 2, 1, 0, False, True),   # tests.rs:457-462, as the reference runs them
+    (64, 16, 0, 1, 2, 2, 1, True, True),
+    (64, 6, 0, 1, 2, 0, 0, True, True),
+    (64, 3, 0, 1, 2, 1, None, False, True),
+    (128, 8, 2, 2, 1, 1, 0, True, False),   # extensions
+    (128, 4, 0, 1, 1, 2, 1, False, False),
+]
+
+
+@pytest.mark.parametrize("case", range(len(STANDALONE)))
+def test_standalone_prologue_is_bit_exact(oracle, torch_gpu, case):
+    import spl_sage as S
+    from spl_sage import qkv as Q
+
+    torch = torch_gpu
+    D, H, kv, B, frames, norm, rope, scaled, head_major = STANDALONE[case]
+    HK = kv or H
+    T = frames * FRAME
+    rng = np.random.default_rng(100 + case)
+    s, y = _spec(oracle, rng, D, H, kv, B, T, norm, rope, scaled)
+    print(f"case {case}: D{D} H{H}/{HK} B{B} T{T} norm {norm} rope {rope} scaled {scaled}", flush=True)
+    inp, qn, rp = _device(torch, s, y)
+    sa = S.SageAttention(None, D)
+    for v_f16 in (False, True):
+        def buf(h, dt):
+            if head_major:
+                t = torch.empty((B, h, T, D), dtype=dt, device="cuda")
+                return t, S.TensorMut(t, S.Strides.bhtd(T, h, D))
+            t = torch.empty((B, T, h, D), dtype=dt, device="cuda")
+            return t, S.TensorMut(t)
+        (q, qm), (k, km), (v, vm) = buf(H, torch.bfloat16), buf(HK, torch.bfloat16), \
+            buf(HK, torch.float16 if v_f16 else torch.bfloat16)
+        Q.QkvPrologue(sa).run(inp, T, H, qn, rp, Q.QkvOut(qm, km, vm), batch=B, kv_heads=kv)
+        torch.cuda.synchronize()
+        s.v_f16 = v_f16
+        want = oracle.qkv_prologue(s, y)
+        for name, got, w in zip("qkv", (q, k, v), want):
+            g = from_device16(got)
+            if head_major:
+                g = np.ascontiguousarray(g.transpose(0, 2, 1, 3))
+            assert np.array_equal(g, w), (name, v_f16, int((g != w).sum()))
+
+
+FUSED = [  # (D, heads, kv, batch, tokens, norm, rope, scaled, causal, merge)
+    (64, 16, 0, 1, 2 * FRAME, 1, 0, True, False, 1),
+    (64, 16, 0, 1, 2 * FRAME, 2, 1, False, False, 4),
+    (128, 8, 2, 2, 1000, 1, 0, True, True, 1),
+    (128, 4, 0, 1, 777, 2, 1, False, False, 1),
+    (128, 4, 4, 1, 300, 0, None, True, False, 1),
+]
+
+
+@pytest.mark.parametrize("case", range(len(FUSED)))
+def test_fused_prepare_equals_the_two_steps(oracle, torch_gpu, case):
+    import spl_sage as S
+    from spl_sage import qkv as Q
+
+    torch = torch_gpu
+    D, H, kv, B, T, norm, rope, scaled, causal, merge = FUSED[case]
+    HK = kv or H
+    rng = np.random.default_rng(200 + case)
+    s, y = _spec(oracle, rng, D, H, kv, B, T, norm, rope, scaled)
+    print(f"case {case}: D{D} H{H}/{HK} B{B} T{T} norm {norm} rope {rope} scaled {scaled} causal {causal} "
+          f"merge {merge}", flush=True)
+    layout = (T // FRAME, SPECIAL, GRID_H, GRID_W, 0) if merge > 1 else (1, 0, 0, 0, 0)
+    p = oracle.Problem(B, H, T, D, kv_heads=kv, dtype=0, causal=causal, merge=merge, layout=layout)
+    q16, k16, v16 = oracle.qkv_prologue(s, y)
+    want = oracle.prologue(p, q16, k16, v16)
+
+    inp, qn, rp = _device(torch, s, y)
+    sa = S.SageAttention(None, D)
+    km = S.KvMerge.Pool(merge, S.FrameLayout(*layout)) if merge > 1 else S.KvMerge.Dense
+    ws = sa.workspace(S.Shape(B, H, T, kv), km)
+    out = torch.empty((B, T, H, D), dtype=torch.bfloat16, device="cuda")
+    sa.forward_qkv(ws, inp, S.TensorMut(out), qn, rp, S.Options(causal=causal))
+    torch.cuda.synchronize()
+    assert_prologue_equal(read_workspace(ws, p), want)
+    o_fused = from_device16(out)
+
+    # the two steps on the GPU: QkvPrologue::run into bf16 Q, K, V, then forward
+    _, o_two = run(torch, p, q16, k16, v16, want_ws=False)
+    assert np.array_equal(o_fused, o_two)
+
+    rows = sample_rows(T, 256, seed=case)
+    _, emu16 = oracle.sage_emulate(p, want, rows=rows, out_dtype=0)
+    e = oracle.errors(oracle.decode16(gather_rows(o_fused, rows), 0), oracle.decode16(emu16, 0))
+    print(f"vs reference arithmetic: {e}")
+    assert e["cos"] >= 0.999 and e["max_abs"] <= 2e-2, e
+
+
+def test_refusals_carry_the_references_text(oracle, torch_gpu):
+    """qkv.rs:226-278: ld, LayerNorm biases, RoPE frame length, buffer sizes."""
+    import spl_sage as S
+    from spl_sage import qkv as Q
+
+    torch = torch_gpu
+    rng = np.random.default_rng(7)
+    s, y = _spec(oracle, rng, 64, 2, 0, 1, 100, 1, 0, False)
+    inp, qn, rp = _device(torch, s, y)
+    sa = S.SageAttention(None, 64)
+    outs = Q.QkvOut(*(S.TensorMut(torch.empty((1, 100, 2, 64), dtype=torch.bfloat16, device="cuda"))
+                      for _ in range(3)))
+    pro = Q.QkvPrologue(sa)
+    bad = Q.QkvIn(inp.y, s.ld + 4, inp.tok, inp.chan, inp.bias)
+    with pytest.raises(S.SageError, match=r"qkv: ld 396 must be a multiple of 8 and at least 384"):
+        pro.run(bad, 100, 2, qn, rp, outs)
+    with pytest.raises(S.SageError, match="qkv: LayerNorm QK-norm needs q and k biases"):
+        pro.run(inp, 100, 2, Q.QkNorm(Q.NormKind.LayerNorm, qn.q_weight, qn.k_weight), rp, outs)
+    with pytest.raises(S.SageError, match="qkv: RoPE frame length is 0"):
+        pro.run(inp, 100, 2, qn, Q.Rope(rp.table, rp.layout, 0), outs)
+    with pytest.raises(S.SageError, match="qkv y: buffer holds"):
+        pro.run(inp, 200, 2, qn, rp, outs)
+    with pytest.raises(S.SageError, match="RoPE table: buffer holds"):
+        pro.run(inp, 100, 2, qn, Q.Rope(rp.table[:100].clone(), rp.layout, FRAME), outs)
+    ws = sa.workspace(S.Shape(1, 2, 100))
+    with pytest.raises(S.SageError, match=r"qkv: ld 396 must be a multiple of 8"):
+        sa.prepare_qkv(ws, bad, qn, rp)
+    pro.run(Q.QkvIn(inp.y, s.ld), 0, 2, None, None, outs)  # empty: a no-op, as the reference

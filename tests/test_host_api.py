@@ -242,3 +242,22 @@ def test_device_gate_without_a_gpu(S):
         pytest.skip("a GPU is present")
     with pytest.raises(S.SageError):
         S.check_device(0)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_rope_tables_match_the_oracle(S, oracle, d):
+    """RopeTable::vggt / ::dinov3 (qkv.rs:87-136) built by the library equal the
+    oracle's restatement, which the reference's own table tests pin; too small
+    an output buffer is refused with the reference's buffer message."""
+    import numpy as np
+
+    from spl_sage import qkv as Q
+
+    for layout in (Q.RopeLayout.Vggt, Q.RopeLayout.Dinov3):
+        t = Q.RopeTable._build(layout, 21, 32, 17, 100.0, d)
+        assert t.frame_len == 17 + 21 * 32
+        assert np.array_equal(t.cos_sin, oracle.rope_table(int(layout), d, 21, 32, 17, 100.0))
+    out = np.empty(10, np.float32)
+    with pytest.raises(S.SageError, match="RoPE table: buffer holds 10 elements, needs"):
+        _check = S._check
+        _check(S.lib().sage_rope_table(0, d, 2, 2, 1, 100.0, out.ctypes.data, out.size))
