@@ -19,6 +19,7 @@
 #include <stdexcept>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "sage_hip.h"
 
@@ -382,5 +383,129 @@ private:
     }
     sage_attention* h_;
 };
+
+// ---------------------------------------------------------------- qkv
+// spl_nn::qkv (platform/spl-nn/src/qkv.rs): the QKV prologue that feeds sage.
+namespace qkv {
+
+constexpr std::size_t HEAD_DIM = 64;  // the reference's head dim; 128 is an extension
+
+// RopeLayout (qkv.rs:33-58).
+enum class RopeLayout : int32_t { Vggt = SAGE_ROPE_VGGT, Dinov3 = SAGE_ROPE_DINOV3 };
+
+inline std::size_t rope_half(RopeLayout l, std::size_t head_dim = HEAD_DIM) {
+    return l == RopeLayout::Vggt ? head_dim / 4 : head_dim / 2;
+}
+inline std::size_t rope_pair(RopeLayout l, std::size_t d, std::size_t head_dim = HEAD_DIM) {
+    const std::size_t h = rope_half(l, head_dim);
+    return (d / (2 * h)) * h + d % h;
+}
+
+// RopeTable (qkv.rs:60-136): cos/sin per (token in frame, pair), host memory.
+struct RopeTable {
+    RopeLayout layout = RopeLayout::Vggt;
+    std::size_t frame_len = 0;
+    std::vector<float> cos_sin;  // frame_len x head_dim/2 x 2
+
+    static RopeTable build(RopeLayout l, std::size_t grid_h, std::size_t grid_w, std::size_t special, double base,
+                           std::size_t head_dim) {
+        RopeTable t;
+        t.layout = l;
+        t.frame_len = special + grid_h * grid_w;
+        t.cos_sin.resize(t.frame_len * head_dim);
+        check(sage_rope_table(static_cast<int32_t>(l), head_dim, grid_h, grid_w, special, base, t.cos_sin.data(),
+                              t.cos_sin.size()));
+        return t;
+    }
+    static RopeTable vggt(std::size_t gh, std::size_t gw, std::size_t special, double base,
+                          std::size_t head_dim = HEAD_DIM) {
+        return build(RopeLayout::Vggt, gh, gw, special, base, head_dim);
+    }
+    static RopeTable dinov3(std::size_t gh, std::size_t gw, std::size_t special, double base,
+                            std::size_t head_dim = HEAD_DIM) {
+        return build(RopeLayout::Dinov3, gh, gw, special, base, head_dim);
+    }
+};
+
+// NormKind / QkNorm (qkv.rs:138-156): device pointers to [head_dim] floats each.
+enum class NormKind : int32_t { LayerNorm = SAGE_QKV_LAYER_NORM, Rms = SAGE_QKV_RMS_NORM };
+struct QkNorm {
+    NormKind kind = NormKind::LayerNorm;
+    const float* q_weight = nullptr;
+    const float* q_bias = nullptr;
+    const float* k_weight = nullptr;
+    const float* k_bias = nullptr;
+    std::size_t len = 0;  // floats each buffer holds
+    float eps = 1e-6f;
+    sage_qkv_norm raw() const {
+        return sage_qkv_norm{static_cast<int32_t>(kind), q_weight, q_bias, k_weight, k_bias, len, eps};
+    }
+};
+
+// Rope (qkv.rs:158-163): the uploaded table (device floats) and its layout.
+struct Rope {
+    const float* table = nullptr;
+    std::size_t table_len = 0;
+    RopeLayout layout = RopeLayout::Vggt;
+    std::size_t frame_len = 0;
+    sage_qkv_rope raw() const {
+        return sage_qkv_rope{table, table_len, static_cast<int32_t>(layout), frame_len};
+    }
+};
+
+// QkvIn (qkv.rs:165-177), with a batch stride (0 = tokens * ld).
+struct QkvIn {
+    const uint16_t* y = nullptr;
+    std::size_t y_len = 0, ld = 0, batch_stride = 0;
+    const float* tok = nullptr;
+    std::size_t tok_len = 0;
+    const float* chan = nullptr;
+    std::size_t chan_len = 0;
+    const uint16_t* bias = nullptr;
+    std::size_t bias_len = 0;
+    sage_qkv_in raw() const {
+        return sage_qkv_in{y, y_len, ld, batch_stride, tok, tok_len, chan, chan_len, bias, bias_len};
+    }
+};
+
+// QkvOut (qkv.rs:188-196): V's dtype is its VFormat (bf16 or fp16).
+struct QkvOut {
+    TensorMut q, k, v;
+};
+
+// QkvPrologue (qkv.rs:198-306) on a SageAttention context's stream and head dim.
+class QkvPrologue {
+public:
+    explicit QkvPrologue(const SageAttention& sa) : sa_(sa) {}
+    void run(const QkvIn& in, std::size_t tokens, std::size_t heads, const QkNorm* norm, const Rope* rope,
+             const QkvOut& out, std::size_t batch = 1, std::size_t kv_heads = 0) const {
+        const sage_shape sh{batch, heads, tokens, kv_heads};
+        const sage_qkv_in i = in.raw();
+        sage_qkv_norm n{};
+        sage_qkv_rope r{};
+        if (norm) n = norm->raw();
+        if (rope) r = rope->raw();
+        const sage_tensor_mut q = out.q.raw(), k = out.k.raw(), v = out.v.raw();
+        check(sage_qkv_prologue(sa_.handle(), &sh, &i, norm ? &n : nullptr, rope ? &r : nullptr, &q, &k, &v));
+    }
+
+private:
+    const SageAttention& sa_;
+};
+
+// The fusion of QkvPrologue::run and SageAttention::prepare (no counterpart in
+// the reference): the same codes, bit for bit, without storing Q, K and V.
+inline void prepare_qkv(const SageAttention& sa, Workspace& ws, const QkvIn& in, const QkNorm* norm, const Rope* rope,
+                        const Options& opts = {}) {
+    const sage_qkv_in i = in.raw();
+    sage_qkv_norm n{};
+    sage_qkv_rope r{};
+    if (norm) n = norm->raw();
+    if (rope) r = rope->raw();
+    const sage_options o = opts.raw();
+    check(sage_prepare_qkv(sa.handle(), ws.handle(), &i, norm ? &n : nullptr, rope ? &r : nullptr, &o));
+}
+
+}  // namespace qkv
 
 }  // namespace spl_sage

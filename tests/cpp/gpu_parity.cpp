@@ -209,8 +209,82 @@ static void run_case(const Case& c) {
     std::fflush(stdout);
 }
 
+// QkvPrologue::run through the C++ qkv mirror (the reference's
+// gpu_qkv_prologue_matches_cpu option sets, tests.rs:447-570, on one 689-token
+// VGGT frame at head dim 64): Q, K and V equal the C oracle's restatement bit
+// for bit, and prepare_qkv's workspace equals prepare's on those Q, K and V.
+static void run_qkv_case(int norm_kind, int layout, bool scaled) {
+    using namespace spl_sage::qkv;
+    const std::size_t d = 64, heads = 4, tokens = 689, width = 3 * heads * d, ld = width + 8;
+    uint64_t st = 1234 + norm_kind * 7 + layout;
+    std::vector<float> yf(tokens * ld), chan(width), tok(tokens), biasf(width), w(4 * d);
+    for (float& x : yf) x = oracle_rng_normal(&st);
+    for (float& x : chan) x = 0.5f + (float)oracle_rng_uniform(&st);
+    for (float& x : tok) x = 0.5f + (float)oracle_rng_uniform(&st);
+    for (float& x : biasf) x = 0.2f * oracle_rng_normal(&st);
+    for (std::size_t i = 0; i < 4 * d; i++) w[i] = (i / d) % 2 == 0 ? 1.0f + 0.2f * oracle_rng_normal(&st)
+                                                                   : 0.1f * oracle_rng_normal(&st);
+    std::vector<uint16_t> y(yf.size()), bias(width);
+    oracle_encode16(yf.data(), y.data(), yf.size(), ORACLE_BF16);
+    oracle_encode16(biasf.data(), bias.data(), width, ORACLE_BF16);
+    const RopeTable table = layout == 0 ? RopeTable::vggt(21, 32, 17, 100.0) : RopeTable::dinov3(21, 32, 17, 100.0);
+
+    DeviceBuf<uint16_t> yd(y.size()), bd(width);
+    DeviceBuf<float> cd(width), td(tokens), wd(4 * d), rd(table.cos_sin.size());
+    hip_ok(hipMemcpy(yd.p, y.data(), y.size() * 2, hipMemcpyHostToDevice), "copy y");
+    hip_ok(hipMemcpy(bd.p, bias.data(), width * 2, hipMemcpyHostToDevice), "copy bias");
+    hip_ok(hipMemcpy(cd.p, chan.data(), width * 4, hipMemcpyHostToDevice), "copy chan");
+    hip_ok(hipMemcpy(td.p, tok.data(), tokens * 4, hipMemcpyHostToDevice), "copy tok");
+    hip_ok(hipMemcpy(wd.p, w.data(), 4 * d * 4, hipMemcpyHostToDevice), "copy norm");
+    hip_ok(hipMemcpy(rd.p, table.cos_sin.data(), table.cos_sin.size() * 4, hipMemcpyHostToDevice), "copy rope");
+
+    QkvIn in;
+    in.y = yd.p, in.y_len = yd.n, in.ld = ld, in.bias = bd.p, in.bias_len = width;
+    if (scaled) in.tok = td.p, in.tok_len = tokens, in.chan = cd.p, in.chan_len = width;
+    spl_sage::qkv::QkNorm qn{norm_kind == 1 ? NormKind::LayerNorm : NormKind::Rms, wd.p, wd.p + d, wd.p + 2 * d, wd.p + 3 * d, d, 1e-6f};
+    const Rope rope{rd.p, rd.n, layout == 0 ? RopeLayout::Vggt : RopeLayout::Dinov3, table.frame_len};
+
+    const SageAttention sage = SageAttention::create(nullptr, d);
+    const std::size_t n = tokens * heads * d;
+    DeviceBuf<uint16_t> q(n), k(n), v(n);
+    const Strides bthd = Strides::bthd(tokens, heads, d);
+    QkvPrologue(sage).run(in, tokens, heads, norm_kind ? &qn : nullptr, &rope,
+                          QkvOut{TensorMut{q.p, n, bthd}, TensorMut{k.p, n, bthd}, TensorMut{v.p, n, bthd}});
+
+    oracle_qkv a{};
+    a.batch = 1, a.tokens = (int)tokens, a.heads = (int)heads, a.kv_heads = (int)heads, a.head_dim = (int)d;
+    a.ld = (long long)ld, a.batch_stride = (long long)(tokens * ld);
+    a.bias = bias.data();
+    if (scaled) a.tok = tok.data(), a.chan = chan.data();
+    a.norm = norm_kind, a.q_w = w.data(), a.q_b = w.data() + d, a.k_w = w.data() + 2 * d, a.k_b = w.data() + 3 * d;
+    a.eps = 1e-6f, a.rope = table.cos_sin.data(), a.rope_layout = layout, a.frame_len = (int)table.frame_len;
+    std::vector<uint16_t> wq(n), wk(n), wv(n);
+    oracle_qkv_prologue(&a, y.data(), wq.data(), wk.data(), wv.data());
+    const auto hq = to_host(q.p, n), hk = to_host(k.p, n), hv = to_host(v.p, n);
+    bool ok = same("q", hq.data(), wq.data(), n) && same("k", hk.data(), wk.data(), n) && same("v", hv.data(), wv.data(), n);
+
+    Workspace ws_two = sage.workspace(Shape{1, heads, tokens}), ws_fused = sage.workspace(Shape{1, heads, tokens});
+    sage.prepare(ws_two, Tensor{q.p, n, bthd}, Tensor{k.p, n, bthd}, Tensor{v.p, n, bthd});
+    prepare_qkv(sage, ws_fused, in, norm_kind ? &qn : nullptr, &rope);
+    const sage_ws_buffers b2 = ws_two.buffers(), b1 = ws_fused.buffers();
+    ok = ok && same("q8", to_host(b1.q8, b1.q8_len).data(), to_host(b2.q8, b2.q8_len).data(), b1.q8_len) &&
+         same("k8", to_host(b1.k8, b1.k8_len).data(), to_host(b2.k8, b2.k8_len).data(), b1.k8_len) &&
+         same("v8", to_host(b1.v8, b1.v8_len).data(), to_host(b2.v8, b2.v8_len).data(), b1.v8_len) &&
+         same("q_scale", to_host(b1.q_scale, b1.q_scale_len).data(), to_host(b2.q_scale, b2.q_scale_len).data(),
+              b1.q_scale_len) &&
+         same("k_scale", to_host(b1.k_scale, b1.k_scale_len).data(), to_host(b2.k_scale, b2.k_scale_len).data(),
+              b1.k_scale_len) &&
+         same("stats", to_host(b1.stats, b1.stats_len).data(), to_host(b2.stats, b2.stats_len).data(), b1.stats_len);
+    std::printf("qkv norm %d rope %d scaled %d: %s\n", norm_kind, layout, (int)scaled, ok ? "bit-exact" : "DIFFERS");
+    if (!ok) failures++;
+    std::fflush(stdout);
+}
+
 int main() {
     check_device(0);
+    run_qkv_case(1, 0, false);
+    run_qkv_case(2, 1, true);
+    run_qkv_case(0, 0, true);
     const FrameLayout small{3, 5, 7, 10, 1};  // tests.rs:596-605
     std::vector<Case> cases;
     for (std::size_t d : {64, 128}) {

@@ -153,6 +153,33 @@ static void v8_positions_are_a_permutation() {
 }
 
 // Options map onto the C struct as the reference's defaults say (mod.rs:326-335).
+// qkv.rs:378-421 (layouts_pair_the_right_channels, vggt_table_matches_its_formula,
+// dinov3_table_matches_its_formula) through the C++ qkv mirror.
+static void qkv_rope_tables() {
+    using namespace spl_sage::qkv;
+    CHECK(rope_pair(RopeLayout::Vggt, 0) == 0 && rope_pair(RopeLayout::Vggt, 16) == 0 &&
+          rope_pair(RopeLayout::Vggt, 15) == 15);
+    CHECK(rope_pair(RopeLayout::Vggt, 32) == 16 && rope_pair(RopeLayout::Vggt, 48) == 16 &&
+          rope_pair(RopeLayout::Vggt, 63) == 31);
+    CHECK(rope_pair(RopeLayout::Dinov3, 0) == 0 && rope_pair(RopeLayout::Dinov3, 32) == 0 &&
+          rope_pair(RopeLayout::Dinov3, 31) == 31 && rope_pair(RopeLayout::Dinov3, 63) == 31);
+    for (RopeLayout l : {RopeLayout::Vggt, RopeLayout::Dinov3})
+        for (std::size_t c = 0; c < HEAD_DIM; c++) CHECK(rope_pair(l, c) == rope_pair(l, c ^ rope_half(l)));
+    const RopeTable t = RopeTable::vggt(3, 4, 2, 100.0);
+    CHECK(t.frame_len == 14);
+    CHECK(t.cos_sin[(1 * 32 + 5) * 2] == 1.0f && t.cos_sin[(1 * 32 + 5) * 2 + 1] == 0.0f);
+    double a = 2.0 * std::pow(100.0, -3.0 / 16.0);
+    CHECK(std::fabs(t.cos_sin[(9 * 32 + 3) * 2] - std::cos(a)) < 1e-7);
+    CHECK(std::fabs(t.cos_sin[(9 * 32 + 3) * 2 + 1] - std::sin(a)) < 1e-7);
+    a = 4.0 * std::pow(100.0, -5.0 / 16.0);
+    CHECK(std::fabs(t.cos_sin[(9 * 32 + 21) * 2 + 1] - std::sin(a)) < 1e-7);
+    const RopeTable d = RopeTable::dinov3(2, 2, 1, 100.0);
+    a = 2.0 * M_PI * -0.5;
+    CHECK(std::fabs(d.cos_sin[(2 * 32 + 0) * 2 + 1] - std::sin(a)) < 1e-7);
+    a = 2.0 * M_PI * 0.5 / std::pow(100.0, 2.0 / 16.0);
+    CHECK(std::fabs(d.cos_sin[(2 * 32 + 18) * 2] - std::cos(a)) < 1e-7);
+}
+
 static void options_defaults() {
     const sage_options o = Options{}.raw();
     CHECK(o.smooth_k == 1 && o.smooth_v == 1 && o.has_softmax_scale == 0 && o.qk_norm_params == nullptr &&
@@ -178,6 +205,7 @@ int main() {
         {"flops_counts_the_pairs", flops_counts_the_pairs},
         {"v8_positions_are_a_permutation", v8_positions_are_a_permutation},
         {"options_defaults", options_defaults},
+        {"qkv_rope_tables", qkv_rope_tables},
     };
     for (auto& t : tests) {
         const int before = failures;
