@@ -8,7 +8,10 @@
 // equal the oracle's prologue bit for bit, the output must reach cos >= 0.999
 // against the oracle's emulation of the reference arithmetic with every
 // element within 2e-2 + 2^-8 |emulated| of it, and the reference's own gate
-// (cos > 0.999, rel_l2 < 0.04) against f64 attention. Prints one line per case; exit status 0 when all pass.
+// (cos > 0.999, rel_l2 < 0.04) against f64 attention. It also runs the
+// reference's caller (sched.rs) through include/spl_sage_sched.hpp, and the
+// QKV prologue through the qkv mirror. Prints one line per case; exit status 0
+// when all pass.
 #include <hip/hip_runtime_api.h>
 
 #include <cmath>
@@ -19,6 +22,7 @@
 
 #include "sage_oracle.h"
 #include "spl_sage.hpp"
+#include "spl_sage_sched.hpp"
 
 using namespace spl_sage;
 
@@ -82,6 +86,78 @@ static bool same(const char* what, const T* a, const T* b, std::size_t n) {
     return false;
 }
 
+// The workspace after a forward, and its bf16 output [B][T][H][d], against
+// the C oracle on the same host inputs (q, k, v with p's strides): every
+// buffer bit for bit, the output within the north-star gate of the emulated
+// reference arithmetic and within the reference's own gate against f64.
+static bool check_forward(const oracle_problem& p, const Workspace& ws, const uint16_t* qh, const uint16_t* kh,
+                          const uint16_t* vh, const uint16_t* dev_out, float scale, bool merged) {
+    const Plan& plan = ws.plan();
+    const std::size_t B = p.batch, H = p.heads, T = p.tokens, d = p.head_dim;
+    const std::size_t tq = plan.tq_pad, tk = plan.tk_pad, nkb = plan.kblocks();
+    std::vector<int8_t> q8(B * H * tq * d), k8(B * H * tk * d);
+    std::vector<float> qs(B * H * tq / QGROUP), ks(B * H * nkb), stats(B * H * 4 * d), kbias(tk);
+    std::vector<uint8_t> v8(B * H * tk * d);
+    if (oracle_prologue(&p, qh, kh, vh, q8.data(), qs.data(), k8.data(), ks.data(), v8.data(), stats.data(),
+                        kbias.data(), 0) != 0) {
+        std::printf("    oracle refused the case\n");
+        return false;
+    }
+
+    // Workspace buffers, bit for bit (v8 back to logical key order).
+    const sage_ws_buffers wb = ws.buffers();
+    bool ok = same("q8", to_host(wb.q8, q8.size()).data(), q8.data(), q8.size());
+    ok &= same("q_scale", to_host(wb.q_scale, qs.size()).data(), qs.data(), qs.size());
+    ok &= same("k8", to_host(wb.k8, k8.size()).data(), k8.data(), k8.size());
+    ok &= same("k_scale", to_host(wb.k_scale, ks.size()).data(), ks.data(), ks.size());
+    ok &= same("stats", to_host(wb.stats, stats.size()).data(), stats.data(), stats.size());
+    {
+        const std::vector<uint8_t> raw = to_host(wb.v8, v8.size());
+        std::vector<uint8_t> logical(v8.size());
+        for (std::size_t bh = 0; bh < B * H; bh++)
+            for (std::size_t blk = 0; blk < nkb; blk++)
+                for (std::size_t ch = 0; ch < d; ch++)
+                    for (int key = 0; key < 64; key++)
+                        logical[(bh * tk + blk * 64 + key) * d + ch] =
+                            raw[((bh * nkb + blk) * d + ch) * 64 + v8_position(key)];
+        ok &= same("v8", logical.data(), v8.data(), v8.size());
+    }
+    if (merged) ok &= same("kbias", to_host(wb.kbias, tk).data(), kbias.data(), tk);
+
+    // Output against the emulation of the reference arithmetic and against f64.
+    const std::vector<uint16_t> o16 = to_host(dev_out, B * T * H * d);
+    std::vector<float> ours(B * H * T * d);
+    for (std::size_t b = 0; b < B; b++)
+        for (std::size_t t = 0; t < T; t++)
+            for (std::size_t h = 0; h < H; h++)
+                oracle_decode16(&o16[((b * T + t) * H + h) * d], &ours[((b * H + h) * T + t) * d], d, ORACLE_BF16);
+    std::vector<float> emu(ours.size()), f64(ours.size());
+    std::vector<uint16_t> emu16(ours.size());
+    oracle_sage_emulate(&p, 0, q8.data(), qs.data(), k8.data(), ks.data(), v8.data(), stats.data(), kbias.data(),
+                        nullptr, (int)T, emu.data(), emu16.data(), ORACLE_BF16, 1, 0);
+    oracle_attention_f64(&p, 0, scale, qh, kh, vh, nullptr, (int)T, f64.data(), 0);
+    // The arithmetic gate compares the bf16 output with the emulation's fp32
+    // output before its own rounding. Data::synthetic outputs reach |out| ~ 10,
+    // where bf16's half step (up to 2^-8 |out|, 2^-5 at 8..16) alone exceeds
+    // 2e-2, so each element is held to 2e-2 + 2^-8 |emu|: the north-star
+    // max-abs bound plus the rounding any bf16 output carries. The
+    // reference's own gate for this data is the f64 one (tests.rs:699).
+    double e[5], e64[5];
+    oracle_errors(ours.data(), emu.data(), ours.size(), e);
+    oracle_errors(ours.data(), f64.data(), ours.size(), e64);
+    std::size_t over = 0;
+    for (std::size_t i = 0; i < ours.size(); i++)
+        if (!(std::fabs(ours[i] - emu[i]) <= 2e-2 + std::ldexp(std::fabs(emu[i]), -8))) over++;
+    const bool gate = e[0] >= 0.999 && over == 0;
+    const bool ref_gate = e64[0] > 0.999 && e64[2] < 0.04;
+    std::printf("    prologue %s; vs reference arithmetic cos %.6f max_abs %.3g (|out| <= %.3g, %zu over the bound) %s; "
+                "vs f64 cos %.6f rel_l2 %.4f %s\n",
+                ok ? "bit-exact" : "DIFFERS", e[0], e[3], e[4], over, gate ? "ok" : "FAIL", e64[0], e64[2],
+                ref_gate ? "ok" : "FAIL");
+    std::fflush(stdout);
+    return ok && gate && ref_gate;
+}
+
 static void run_case(const Case& c) {
     std::printf("case %s\n", c.name.c_str());
     std::fflush(stdout);
@@ -110,7 +186,6 @@ static void run_case(const Case& c) {
     if (c.pv16) cfg.pv_accum = PvAccum::F16;
     const SageAttention sage = SageAttention::with_config(nullptr, d, cfg);
     Workspace ws = sage.workspace(shape, c.merge);
-    const Plan& plan = ws.plan();
     const Strides st = Strides::packed_qkv(T, H, d);
     Options opts;
     opts.smooth_k = opts.smooth_v = c.smooth;
@@ -143,70 +218,8 @@ static void run_case(const Case& c) {
     p.ln = c.ln ? lnp.data() : nullptr;
     p.ln_eps = 1e-5f;
     p.pv16 = c.pv16 ? 1 : 0;
-    const std::size_t tq = plan.tq_pad, tk = plan.tk_pad, nkb = plan.kblocks();
-    std::vector<int8_t> q8(B * H * tq * d), k8(B * H * tk * d);
-    std::vector<float> qs(B * H * tq / QGROUP), ks(B * H * nkb), stats(B * H * 4 * d), kbias(tk);
-    std::vector<uint8_t> v8(B * H * tk * d);
     const uint16_t* hp = packed.data();
-    if (oracle_prologue(&p, hp, hp + hd, hp + 2 * hd, q8.data(), qs.data(), k8.data(), ks.data(), v8.data(),
-                        stats.data(), kbias.data(), 0) != 0) {
-        std::printf("    oracle refused the case\n");
-        failures++;
-        return;
-    }
-
-    // Workspace buffers, bit for bit (v8 back to logical key order).
-    const sage_ws_buffers wb = ws.buffers();
-    bool ok = same("q8", to_host(wb.q8, q8.size()).data(), q8.data(), q8.size());
-    ok &= same("q_scale", to_host(wb.q_scale, qs.size()).data(), qs.data(), qs.size());
-    ok &= same("k8", to_host(wb.k8, k8.size()).data(), k8.data(), k8.size());
-    ok &= same("k_scale", to_host(wb.k_scale, ks.size()).data(), ks.data(), ks.size());
-    ok &= same("stats", to_host(wb.stats, stats.size()).data(), stats.data(), stats.size());
-    {
-        const std::vector<uint8_t> raw = to_host(wb.v8, v8.size());
-        std::vector<uint8_t> logical(v8.size());
-        for (std::size_t bh = 0; bh < B * H; bh++)
-            for (std::size_t blk = 0; blk < nkb; blk++)
-                for (std::size_t ch = 0; ch < d; ch++)
-                    for (int key = 0; key < 64; key++)
-                        logical[(bh * tk + blk * 64 + key) * d + ch] =
-                            raw[((bh * nkb + blk) * d + ch) * 64 + v8_position(key)];
-        ok &= same("v8", logical.data(), v8.data(), v8.size());
-    }
-    if (!c.merge.is_dense()) ok &= same("kbias", to_host(wb.kbias, tk).data(), kbias.data(), tk);
-
-    // Output against the emulation of the reference arithmetic and against f64.
-    const std::vector<uint16_t> o16 = to_host(dout.p, dout.n);
-    std::vector<float> ours(B * H * T * d);
-    for (std::size_t b = 0; b < B; b++)
-        for (std::size_t t = 0; t < T; t++)
-            for (std::size_t h = 0; h < H; h++)
-                oracle_decode16(&o16[((b * T + t) * H + h) * d], &ours[((b * H + h) * T + t) * d], d, ORACLE_BF16);
-    std::vector<float> emu(ours.size()), f64(ours.size());
-    std::vector<uint16_t> emu16(ours.size());
-    oracle_sage_emulate(&p, 0, q8.data(), qs.data(), k8.data(), ks.data(), v8.data(), stats.data(), kbias.data(),
-                        nullptr, (int)T, emu.data(), emu16.data(), ORACLE_BF16, 1, 0);
-    oracle_attention_f64(&p, 0, scale, hp, hp + hd, hp + 2 * hd, nullptr, (int)T, f64.data(), 0);
-    // The arithmetic gate compares the bf16 output with the emulation's fp32
-    // output before its own rounding. Data::synthetic outputs reach |out| ~ 10,
-    // where bf16's half step (up to 2^-8 |out|, 2^-5 at 8..16) alone exceeds
-    // 2e-2, so each element is held to 2e-2 + 2^-8 |emu|: the north-star
-    // max-abs bound plus the rounding any bf16 output carries. The
-    // reference's own gate for this data is the f64 one (tests.rs:699).
-    double e[5], e64[5];
-    oracle_errors(ours.data(), emu.data(), ours.size(), e);
-    oracle_errors(ours.data(), f64.data(), ours.size(), e64);
-    std::size_t over = 0;
-    for (std::size_t i = 0; i < ours.size(); i++)
-        if (!(std::fabs(ours[i] - emu[i]) <= 2e-2 + std::ldexp(std::fabs(emu[i]), -8))) over++;
-    const bool gate = e[0] >= 0.999 && over == 0;
-    const bool ref_gate = e64[0] > 0.999 && e64[2] < 0.04;
-    std::printf("    prologue %s; vs reference arithmetic cos %.6f max_abs %.3g (|out| <= %.3g, %zu over the bound) %s; "
-                "vs f64 cos %.6f rel_l2 %.4f %s\n",
-                ok ? "bit-exact" : "DIFFERS", e[0], e[3], e[4], over, gate ? "ok" : "FAIL", e64[0], e64[2],
-                ref_gate ? "ok" : "FAIL");
-    if (!ok || !gate || !ref_gate) failures++;
-    std::fflush(stdout);
+    if (!check_forward(p, ws, hp, hp + hd, hp + 2 * hd, dout.p, scale, !c.merge.is_dense())) failures++;
 }
 
 // QkvPrologue::run through the C++ qkv mirror (the reference's
@@ -280,8 +293,104 @@ static void run_qkv_case(int norm_kind, int layout, bool scaled) {
     std::fflush(stdout);
 }
 
+// The reference's caller (apps/image-to-3d/src/vggt/trunk/sched.rs) through its
+// C++ restatement (include/spl_sage_sched.hpp): the shipped `ours+sage` schedule
+// (vggt/mod.rs:82-107: frame attention at 3-5, merge4 at 0, 1, 7, 19, register
+// attention at 2, 6, 9, 14, 20, the other global layers through sage) at a
+// 3-frame VGGT geometry of 7 x 10 patches. Sage::prepare makes one workspace per
+// distinct merge, each the size the caller counts (sched.rs:56-71); each sage
+// layer runs SageLayer::forward on head-major bf16 Q, K and V (Data::synthetic,
+// seed 17) and is checked against the oracle; the caller's errors carry its texts.
+static void run_sched_case() {
+    using namespace spl_vggt;
+    std::printf("case sched: ours+sage schedule, VGGT geometry 3 frames x (17 + 7 x 10)\n");
+    std::fflush(stdout);
+    const TrunkGeom g{3, 7, 10};
+    const std::size_t T = g.rows(), H = HEADS, d = HEAD_DIM, n = H * T * d;
+    Schedule sched;
+    sched.fill(InterKind::Global);
+    for (std::size_t i : {2, 6, 9, 14, 20}) sched[i] = InterKind::Register;
+    for (InterKind& a : sched)
+        if (a == InterKind::Global) a = InterKind::Sage;
+    for (std::size_t i : {3, 4, 5}) sched[i] = InterKind::Frame;
+    for (std::size_t i : {0, 1, 7, 19}) sched[i] = InterKind::Merge4;
+
+    Sage sage;
+    sage.prepare(nullptr, sched, g);
+    bool ok = sage.workspaces() == 2;
+
+    std::vector<uint16_t> q(n), k(n), v(n), qh(n), kh(n), vh(n);
+    oracle_reference_synthetic(1, (int)T, (int)H, (int)d, 17, q.data(), k.data(), v.data());
+    for (std::size_t t = 0; t < T; t++)
+        for (std::size_t h = 0; h < H; h++) {
+            std::memcpy(&qh[(h * T + t) * d], &q[(t * H + h) * d], d * 2);
+            std::memcpy(&kh[(h * T + t) * d], &k[(t * H + h) * d], d * 2);
+            std::memcpy(&vh[(h * T + t) * d], &v[(t * H + h) * d], d * 2);
+        }
+    DeviceBuf<uint16_t> dq(n), dk(n), dv(n), dout(n);
+    hip_ok(hipMemcpy(dq.p, qh.data(), n * 2, hipMemcpyHostToDevice), "upload q");
+    hip_ok(hipMemcpy(dk.p, kh.data(), n * 2, hipMemcpyHostToDevice), "upload k");
+    hip_ok(hipMemcpy(dv.p, vh.data(), n * 2, hipMemcpyHostToDevice), "upload v");
+
+    for (InterKind kind : {InterKind::Sage, InterKind::Merge4}) {
+        const KvMerge m = *merge_of(kind, g);
+        const SageLayer layer = sage.layer(kind, g);
+        ok &= layer.v_format() == Dtype::Bf16;
+        const std::size_t bytes = layer.workspace().bytes(), want = workspace_bytes(g, m);
+        std::printf("  %s layer: workspace %zu bytes (the caller counts %zu)\n", kind_name(kind), bytes, want);
+        ok &= bytes == want;
+        layer.forward(dq.p, n, dk.p, n, dv.p, n, dout.p, n, 1, T);
+        hip_ok(hipDeviceSynchronize(), "sage layer forward");
+        oracle_problem p{};
+        p.batch = 1;
+        p.heads = p.kv_heads = (int)H;
+        p.tokens = (int)T;
+        p.head_dim = (int)d;
+        p.dtype = ORACLE_BF16;
+        p.q_sb = p.k_sb = p.v_sb = (long long)(H * T * d);
+        p.q_st = p.k_st = p.v_st = (long long)d;
+        p.q_sh = p.k_sh = p.v_sh = (long long)(T * d);
+        p.q_mul = ATTN_SCALE * 1.44269504088896340736f;
+        p.smooth_k = p.smooth_v = 1;
+        p.v_range = FP8_MAX;
+        p.merge = (int)m.stride;
+        p.frames = (int)m.layout.frames;
+        p.special = (int)m.layout.special;
+        p.grid_h = (int)m.layout.grid_h;
+        p.grid_w = (int)m.layout.grid_w;
+        p.dense_frames = (int)m.layout.dense_frames;
+        p.ln_eps = 1e-5f;
+        ok &= check_forward(p, layer.workspace(), qh.data(), kh.data(), vh.data(), dout.p, ATTN_SCALE, !m.is_dense());
+    }
+    // The caller's refusals (sched.rs:150-164, 189-195).
+    auto refuses = [&](auto f, const std::string& text) {
+        try {
+            f();
+        } catch (const Error& e) {
+            const bool hit = std::string(e.what()) == text;
+            std::printf("  refused: \"%s\"%s\n", e.what(), hit ? "" : " (unexpected text)");
+            return hit;
+        }
+        std::printf("  no error (expected \"%s\")\n", text.c_str());
+        return false;
+    };
+    ok &= refuses([&] { sage.layer(InterKind::Sage, g).forward(dq.p, n, dk.p, n, dv.p, n, dout.p, n, 2, T / 2); },
+                  "sage layer: workspace for Shape { batch: 1, heads: 16, tokens: 261 }, called with 2 \xc3\x97 130");
+    ok &= refuses([&] { sage.layer(InterKind::Merge2, g); },
+                  "sage workspace for Merge2 at TrunkGeom { frames: 3, grid_h: 7, grid_w: 10 } not prepared");
+    ok &= refuses([&] { sage.layer(InterKind::Frame, g); }, "Frame is not a sage layer");
+    // A new geometry drops the old workspaces; one frame has nothing to merge.
+    const TrunkGeom one{1, 7, 10};
+    sage.prepare(nullptr, sched, one);
+    ok &= sage.workspaces() == 1 && sage.layer(InterKind::Merge4, one).workspace().plan().merge.is_dense();
+    std::printf("  %s\n", ok ? "ok" : "FAIL");
+    if (!ok) failures++;
+    std::fflush(stdout);
+}
+
 int main() {
     check_device(0);
+    run_sched_case();
     run_qkv_case(1, 0, false);
     run_qkv_case(2, 1, true);
     run_qkv_case(0, 0, true);

@@ -9,6 +9,7 @@
 #include <type_traits>
 
 #include "spl_sage.hpp"
+#include "spl_sage_sched.hpp"
 
 using namespace spl_sage;
 
@@ -191,6 +192,51 @@ static void options_defaults() {
     CHECK(w.has_softmax_scale == 1 && w.softmax_scale == 0.125f && w.qk_norm_len == 256 && w.qk_norm_eps == 1e-6f);
 }
 
+// The reference's caller (apps/image-to-3d/src/vggt/trunk/sched.rs) through
+// include/spl_sage_sched.hpp, host side: merge_of for every schedule entry
+// (sched.rs:24-46), merges of the shipped `ours+sage` schedule (vggt/mod.rs:
+// 82-107) in first-use order (sched.rs:73-85), and the refusals Sage::layer
+// makes before any kernel exists (sched.rs:150-158).
+static void vggt_caller_schedule() {
+    using namespace spl_vggt;
+    const TrunkGeom g{200, 21, 32};
+    CHECK(g.tokens() == 689 && g.rows() == 137800);
+    CHECK(merge_of(InterKind::Sage, g)->is_dense());
+    for (InterKind k : {InterKind::Global, InterKind::Register, InterKind::Frame}) CHECK(!merge_of(k, g));
+    const std::optional<KvMerge> m4 = merge_of(InterKind::Merge4, g), m2 = merge_of(InterKind::Merge2, g);
+    CHECK(m4 && m4->stride == 4 && m4->layout.frames == 200 && m4->layout.special == 17 && m4->layout.grid_h == 21 &&
+          m4->layout.grid_w == 32 && m4->layout.dense_frames == 1);
+    CHECK(m2 && m2->stride == 2 && !same_merge(*m2, *m4));
+    // One frame has nothing to merge: frame 0 stays dense.
+    const TrunkGeom one{1, 21, 32};
+    CHECK(merge_of(InterKind::Merge4, one)->is_dense() && merge_of(InterKind::Merge2, one)->is_dense());
+    // The plan of a merge4 layer at 200 frames: 689 dense keys + 199 x (17 + 6 x 8) pooled.
+    CHECK(Plan::create(shape(g), *m4).tk == 689 + 199 * 65);
+
+    Schedule sched;
+    sched.fill(InterKind::Global);
+    for (std::size_t i : {2, 6, 9, 14, 20}) sched[i] = InterKind::Register;
+    for (InterKind& a : sched)
+        if (a == InterKind::Global) a = InterKind::Sage;
+    for (std::size_t i : {3, 4, 5}) sched[i] = InterKind::Frame;
+    for (std::size_t i : {0, 1, 7, 19}) sched[i] = InterKind::Merge4;
+    const std::vector<KvMerge> need = merges(sched, g);
+    CHECK(need.size() == 2 && need[0].stride == 4 && need[1].is_dense());
+    CHECK(merges(sched, one).size() == 1);
+    Schedule frames_only;
+    frames_only.fill(InterKind::Frame);
+    CHECK(merges(frames_only, g).empty());
+    // The caller's byte count: positive for its plans, 0 for a refused one.
+    CHECK(workspace_bytes(g, need[0]) > 0 && workspace_bytes(g, need[1]) > workspace_bytes(g, need[0]));
+    CHECK(workspace_bytes(TrunkGeom{0, 21, 32}, KvMerge::Dense()) == 0);
+
+    Sage sage;
+    sage.prepare(nullptr, frames_only, g);  // nothing to prepare: no kernels, no workspaces
+    CHECK(sage.kernels() == nullptr && sage.workspaces() == 0);
+    EXPECT_ERROR(sage.layer(InterKind::Global, g), SAGE_ERR_INVALID, "Global is not a sage layer");
+    EXPECT_ERROR(sage.layer(InterKind::Merge4, g), SAGE_ERR_STATE, "sage kernels not prepared");
+}
+
 int main() {
     struct {
         const char* name;
@@ -206,6 +252,7 @@ int main() {
         {"v8_positions_are_a_permutation", v8_positions_are_a_permutation},
         {"options_defaults", options_defaults},
         {"qkv_rope_tables", qkv_rope_tables},
+        {"vggt_caller_schedule", vggt_caller_schedule},
     };
     for (auto& t : tests) {
         const int before = failures;

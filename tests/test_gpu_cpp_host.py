@@ -2,7 +2,9 @@
 tests/cpp/bin/gpu_parity, the reference's gpu_prologue_matches_reference and
 gpu_attention_matches_float_reference (tests.rs:606-700) restated in C++ with
 the C oracle as checker: workspace buffers bit-exact, outputs within the
-north-star gate of the reference arithmetic and the reference's f64 gate."""
+north-star gate of the reference arithmetic and the reference's f64 gate. It
+also runs the reference's caller, the VGGT trunk's sage scheduler (sched.rs),
+restated in include/spl_sage_sched.hpp, on the shipped `ours+sage` schedule."""
 from __future__ import annotations
 
 import subprocess
