@@ -70,3 +70,43 @@ def test_causal_over_merged_keys_is_refused(oracle, torch_gpu):
     with pytest.raises(S.SageError) as err:
         sa.prepare(ws, S.Tensor(x), S.Tensor(x), S.Tensor(x), S.Options(causal=True))
     assert err.value.status == 2 and "merged keys" in str(err.value)
+
+
+@pytest.mark.parametrize("stride", [2, 4])
+@pytest.mark.parametrize("d", [64, 128])
+def test_merged_attention_equals_dense_on_uniform_cells(oracle, torch_gpu, stride, d):
+    """merged_attention_equals_dense_on_uniform_cells (tests.rs:193-232) through
+    the GPU path: when every pooled cell holds identical keys and values,
+    attention over the pooled keys with the log2-count bias is attention over
+    all keys. Both runs quantise, and their 64-key blocks (hence their K scales
+    and the running maxima their P grids follow) differ, so the two agree to
+    the algorithm's own quantisation error rather than bit for bit: on the
+    CPU emulator they differ by cos 0.9998 and max-abs up to 0.33 at outputs of
+    3.7, each at cos 0.9994 against f64. Here: cos >= 0.999 and rel_l2 < 0.04
+    between them, and each within the reference's gate against f64 dense
+    attention (cos > 0.999, rel_l2 < 0.04, tests.rs:699)."""
+    lay = (3, 5, 7, 10, 0)
+    p = _merged(oracle, stride, lay, 2, d, softmax_scale=0.25)
+    dense = oracle.Problem(1, 2, p.tokens, d, softmax_scale=0.25)
+    rng = np.random.default_rng(7 + stride)
+    cell_k = rng.standard_normal((2, p.tk, d)).astype(np.float32)
+    cell_v = rng.standard_normal((2, p.tk, d)).astype(np.float32)
+    k = np.zeros((1, p.tokens, 2, d), np.float32)
+    v = np.zeros_like(k)
+    for j in range(p.tk):
+        for t in p.members(j):
+            k[0, t] = cell_k[:, j]
+            v[0, t] = cell_v[:, j]
+    q = (2.0 * rng.standard_normal((1, p.tokens, 2, d))).astype(np.float32)
+    q16, k16, v16 = (oracle.encode16(x, 0) for x in (q, k, v))
+    _, om = run(torch_gpu, p, q16, k16, v16, want_ws=False)
+    _, od = run(torch_gpu, dense, q16, k16, v16, want_ws=False)
+    rows = np.arange(p.tokens)
+    merged_out = oracle.decode16(gather_rows(om, rows), 0)
+    dense_out = oracle.decode16(gather_rows(od, rows), 0)
+    e = oracle.errors(merged_out, dense_out)
+    assert e["cos"] >= 0.999 and e["rel_l2"] < 0.04, e
+    exact = oracle.attention_f64(dense, q16, k16, v16)
+    for out in (merged_out, dense_out):
+        e64 = oracle.errors(out, exact)
+        assert e64["cos"] > 0.999 and e64["rel_l2"] < 0.04, e64
