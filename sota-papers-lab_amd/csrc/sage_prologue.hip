@@ -402,14 +402,60 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
         mv[e] = st[D + ch * 8 + e];
         iv[e] = st[3 * D + ch * 8 + e];
     }
-    QkvLane lk, lv;
-    if (QKV) {
-        qkv_lane<D>(lk, qa, g, 1, hk, ch);
-        qkv_lane<D>(lv, qa, g, 2, hk, ch);
-    }
     float kv[NI][8];
     float amax = 0.f;
-    if (g.merge == 1) {
+    if (QKV && g.merge == 1) {
+        // Rows of the fused projection: V first, then K, so that only one
+        // part's channel constants (QkvLane) and statistics are live at a time.
+        __syncthreads();
+        {
+            QkvLane lv;
+            qkv_lane<D>(lv, qa, g, 2, hk, ch);
+            uint4 vraw[NI];
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int j = blk * KBLOCK + slot + i * TPI;
+                vraw[i] = load16(v + b * g.v_sb + (long long)j * g.v_st + hk * g.v_sh + ch * 8, j < g.tk);
+            }
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int kl = slot + i * TPI;
+                const bool ok = blk * KBLOCK + kl < g.tk;
+                float fv[8], vq[8];
+                unpack8(vraw[i], fv, false);
+                QkvTok tt;
+                qkv_tok<D>(tt, qa, g, 2, b, blk * KBLOCK + kl, ch);
+                qkv_row<D>(fv, qa, lv, tt, 2, ch);
+#pragma unroll
+                for (int e = 0; e < 8; e++) vq[e] = ok ? ((fv[e] + 0.0f) - mv[e]) * iv[e] : 0.f;
+                put_v(vt, ch, kl, vq);
+            }
+        }
+        QkvLane lk;
+        qkv_lane<D>(lk, qa, g, 1, hk, ch);
+        uint4 kraw[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int j = blk * KBLOCK + slot + i * TPI;
+            kraw[i] = load16(k + b * g.k_sb + (long long)j * g.k_st + hk * g.k_sh + ch * 8, j < g.tk);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int kl = slot + i * TPI;
+            const bool ok = blk * KBLOCK + kl < g.tk;
+            float fk[8];
+            unpack8(kraw[i], fk, false);
+            QkvTok tt;
+            qkv_tok<D>(tt, qa, g, 1, b, blk * KBLOCK + kl, ch);
+            qkv_row<D>(fk, qa, lk, tt, 1, ch);
+            if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                kv[i][e] = ok ? (fk[e] + 0.0f) - mk[e] : 0.f;
+                amax = fmaxf(amax, fabsf(kv[i][e]));
+            }
+        }
+    } else if (g.merge == 1) {
         uint4 kraw[NI], vraw[NI];
 #pragma unroll
         for (int i = 0; i < NI; i++) {
@@ -426,12 +472,6 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
             float fk[8], fv[8];
             unpack8(kraw[i], fk, f16);
             unpack8(vraw[i], fv, f16);
-            if (QKV) {
-                QkvTok tt;
-                qkv_tok<D>(tt, qa, g, 1, b, blk * KBLOCK + kl, ch);
-                qkv_row<D>(fk, qa, lk, tt, 1, ch);
-                qkv_row<D>(fv, qa, lv, tt, 2, ch);
-            }
             if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
             float vq[8];
 #pragma unroll
@@ -446,6 +486,75 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
     } else {
         __syncthreads();
         const int cells = g.merge * g.merge;  // uniform bound of the member loop
+        if constexpr (QKV) {
+            // Members of the fused projection: V then K, as in the dense path.
+            {
+                QkvLane lv;
+                qkv_lane<D>(lv, qa, g, 2, hk, ch);
+#pragma unroll
+                for (int i = 0; i < NI; i++) {
+                    const int kl = slot + i * TPI;
+                    const int j = blk * KBLOCK + kl;
+                    const bool ok = j < g.tk;
+                    int base = 0, nx = 1;
+                    const int cnt = ok ? merged_members(g, j, base, nx) : 0;
+                    float vs[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) vs[e] = 0.f;
+                    for (int m = 0; m < cells; m++) {
+                        const bool mok = m < cnt;
+                        const int tok = base + (mok ? (m / nx) * g.grid_w + m % nx : 0);
+                        float fv[8];
+                        unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, mok), fv, false);
+                        QkvTok tt;
+                        qkv_tok<D>(tt, qa, g, 2, b, tok, ch);
+                        qkv_row<D>(fv, qa, lv, tt, 2, ch);
+                        if (mok) {
+#pragma unroll
+                            for (int e = 0; e < 8; e++) vs[e] += fv[e];
+                        }
+                    }
+                    const float rc = cnt > 0 ? 1.0f / (float)cnt : 0.f;
+                    float vq[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) vq[e] = ok ? __builtin_fmaf(vs[e], rc, -mv[e]) * iv[e] : 0.f;
+                    put_v(vt, ch, kl, vq);
+                }
+            }
+            QkvLane lk;
+            qkv_lane<D>(lk, qa, g, 1, hk, ch);
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int kl = slot + i * TPI;
+                const int j = blk * KBLOCK + kl;
+                const bool ok = j < g.tk;
+                int base = 0, nx = 1;
+                const int cnt = ok ? merged_members(g, j, base, nx) : 0;
+                float ks[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) ks[e] = 0.f;
+                for (int m = 0; m < cells; m++) {
+                    const bool mok = m < cnt;
+                    const int tok = base + (mok ? (m / nx) * g.grid_w + m % nx : 0);
+                    float fk[8];
+                    unpack8(load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, mok), fk, false);
+                    QkvTok tt;
+                    qkv_tok<D>(tt, qa, g, 1, b, tok, ch);
+                    qkv_row<D>(fk, qa, lk, tt, 1, ch);
+                    if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
+                    if (mok) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) ks[e] += fk[e];
+                    }
+                }
+                const float rc = cnt > 0 ? 1.0f / (float)cnt : 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    kv[i][e] = ok ? __builtin_fmaf(ks[e], rc, -mk[e]) : 0.f;
+                    amax = fmaxf(amax, fabsf(kv[i][e]));
+                }
+            }
+        } else {
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int kl = slot + i * TPI;
@@ -462,12 +571,6 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
                 float fk[8], fv[8];
                 unpack8(load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, mok), fk, f16);
                 unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, mok), fv, f16);
-                if (QKV) {
-                    QkvTok tt;
-                    qkv_tok<D>(tt, qa, g, 1, b, tok, ch);
-                    qkv_row<D>(fk, qa, lk, tt, 1, ch);
-                    qkv_row<D>(fv, qa, lv, tt, 2, ch);
-                }
                 if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
                 if (mok) {
 #pragma unroll
@@ -486,6 +589,7 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
                 vq[e] = ok ? __builtin_fmaf(vs[e], rc, -mv[e]) * iv[e] : 0.f;
             }
             put_v(vt, ch, kl, vq);
+        }
         }
     }
     amax = wave_max(amax);
