@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <new>
 #include <string>
 
 #include "sage_device.hpp"
@@ -253,7 +254,9 @@ sage_status sage_new(void* stream, uint64_t head_dim, const sage_config* config,
     if (e != hipSuccess) return hip_fail(e, "current device");
     st = sage_check_device(dev);
     if (st != SAGE_OK) return st;
-    sage_attention* s = new sage_attention;
+    // No C++ exception may cross the C ABI: allocation failure is a status.
+    sage_attention* s = new (std::nothrow) sage_attention;
+    if (!s) return fail(SAGE_ERR_DEVICE, "out of host memory");
     s->stream = static_cast<hipStream_t>(stream);
     s->device = dev;
     s->head_dim = head_dim;
@@ -351,7 +354,8 @@ sage_status sage_workspace_new(const sage_attention* s, const sage_shape* shape,
     sage::WsSizes n;
     sage_status st = sage::workspace_layout(s, shape, merge, &plan, &n);
     if (st != SAGE_OK) return st;
-    sage_workspace* w = new sage_workspace;
+    sage_workspace* w = new (std::nothrow) sage_workspace;
+    if (!w) return fail(SAGE_ERR_DEVICE, "out of host memory");
     w->plan = plan;
     w->head_dim = s->head_dim;
     w->device = s->device;
