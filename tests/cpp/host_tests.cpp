@@ -229,6 +229,13 @@ static void vggt_caller_schedule() {
     // The caller's byte count: positive for its plans, 0 for a refused one.
     CHECK(workspace_bytes(g, need[0]) > 0 && workspace_bytes(g, need[1]) > workspace_bytes(g, need[0]));
     CHECK(workspace_bytes(TrunkGeom{0, 21, 32}, KvMerge::Dense()) == 0);
+    // sage_workspaces_are_counted (phase2_tests.rs:98-117): the phase-2 schedule's
+    // workspaces (dense sage: Q, K and V at a byte each; merge4: Q and pooled K/V)
+    // add between 4 and 5 bytes per (head, channel, token) at 200 frames.
+    std::size_t extra = 0;
+    for (const KvMerge& m : need) extra += workspace_bytes(g, m);
+    const std::size_t per = std::size_t(16) * 64 * 200 * 689;
+    CHECK(extra > 4 * per && extra < 5 * per);
 
     Sage sage;
     sage.prepare(nullptr, frames_only, g);  // nothing to prepare: no kernels, no workspaces
