@@ -661,7 +661,16 @@ sage_status qkv_setup(uint64_t batch, uint64_t tokens, uint64_t heads, uint64_t 
         if (!aligned(rope->table, 16, &st)) return st;
         qa->rope = rope->table;
         qa->rope_half = (int)(rope->layout == SAGE_ROPE_VGGT ? d / 4 : d / 2);
+        qa->rope_shift = 0;
+        while ((1 << qa->rope_shift) < qa->rope_half) qa->rope_shift++;
         qa->frame_len = (int)rope->frame_len;
+        // The kernels' t % frame_len by multiplication (Granlund-Montgomery,
+        // the form documented at QkvDev::fl_magic).
+        const uint64_t fl = rope->frame_len;
+        int l = 0;
+        while ((1ull << l) < fl) l++;
+        qa->fl_shift = l;
+        qa->fl_magic = (uint32_t)(((1ull << 32) * ((1ull << l) - fl)) / fl + 1);
     }
     if (!aligned(in->y, 16, &st) || (in->chan && !aligned(in->chan, 16, &st)) ||
         (in->bias && !aligned(in->bias, 16, &st)) || (in->tok && !aligned(in->tok, 4, &st)))

@@ -148,10 +148,24 @@ struct QkvDev {
     const float* nw[4];    // [D] each: q weight, q bias, k weight, k bias (biases: LayerNorm)
     const float* rope;     // [frame_len][D / 2][2]: cos, sin of each rotation pair
     int norm;              // 0 none, 1 LayerNorm, 2 RMSNorm
-    int rope_half;         // channels between the two of a rotation pair
+    int rope_half;         // channels between the two of a rotation pair (a power of two)
+    int rope_shift;        // log2(rope_half)
     int frame_len;         // rope row of token t: t % frame_len
+    // t / frame_len for 0 <= t < 2^31 as (umulhi(fl_magic, t) + t) >> fl_shift
+    // (Granlund and Montgomery, "Division by Invariant Integers using
+    // Multiplication", 1994, fig. 4.1: l = ceil(log2 frame_len), magic =
+    // floor(2^32 (2^l - frame_len) / frame_len) + 1; the sum stays below 2^32).
+    uint32_t fl_magic;
+    int fl_shift;
     float eps;
 };
+
+// The RoPE table row of token t (t % frame_len) without a runtime divide.
+__device__ __forceinline__ int rope_row(const QkvDev& a, int t) {
+    const uint32_t n = (uint32_t)t;
+    const uint32_t q = (__umulhi(a.fl_magic, n) + n) >> a.fl_shift;
+    return (int)(n - q * (uint32_t)a.frame_len);
+}
 
 // The QKV prologue (qkv.cu:50-120) on one (token, part, head) row whose D
 // channels lie on D/8 consecutive lanes, 8 a lane (ch = the lane's chunk;
@@ -222,9 +236,10 @@ template <int D>
 __device__ __forceinline__ void qkv_tok(QkvTok& T, const QkvDev& a, const Geom& g, int part, int b, int tok, int ch) {
     if (a.tok) T.t = a.tok[(long long)b * g.tokens + min(tok, g.tokens - 1)];
     if (a.rope && part < 2) {
-        const int half = a.rope_half, d0 = ch * 8;
-        const int pair0 = (d0 / (2 * half)) * half + d0 % half;
-        const float4* row = reinterpret_cast<const float4*>(a.rope + (long long)(tok % a.frame_len) * D + 2 * pair0);
+        // Pair of the lane's first channel: (d0 / (2 half)) half + d0 % half.
+        const int d0 = ch * 8, sh = a.rope_shift;
+        const int pair0 = ((d0 >> (sh + 1)) << sh) + (d0 & (a.rope_half - 1));
+        const float4* row = reinterpret_cast<const float4*>(a.rope + (long long)rope_row(a, tok) * D + 2 * pair0);
 #pragma unroll
         for (int i = 0; i < 4; i++) T.cs[i] = row[i];
     }
