@@ -10,6 +10,7 @@ platform/spl-nn/src/qkv.rs, cuda/qkv.cu), through the C ABI:
   oracle prologue of the oracle QKV prologue's bf16 Q, K and V bit for bit,
   and the attention output equals the unfused GPU path (sage_qkv_prologue,
   then prepare and attend) bit for bit, and meets the north-star gate;
+- RoPE rows t % frame_len at frame lengths 1, 38, 64 and 4096, both paths;
 - the reference's refusals, before any launch."""
 from __future__ import annotations
 
@@ -25,7 +26,7 @@ GRID_H, GRID_W, SPECIAL = 21, 32, 17
 FRAME = SPECIAL + GRID_H * GRID_W  # 689
 
 
-def _spec(O, rng, D, heads, kv, batch, tokens, norm, rope, scaled, ld_pad=8):
+def _spec(O, rng, D, heads, kv, batch, tokens, norm, rope, scaled, ld_pad=8, grid=(GRID_H, GRID_W, SPECIAL)):
     s = O.QkvSpec(batch, tokens, heads, D, kv_heads=kv)
     s.ld = s.width + ld_pad
     if scaled:
@@ -37,7 +38,7 @@ def _spec(O, rng, D, heads, kv, batch, tokens, norm, rope, scaled, ld_pad=8):
         s.norm_w = np.stack([1 + 0.2 * rng.standard_normal(D), 0.1 * rng.standard_normal(D),
                              1 + 0.2 * rng.standard_normal(D), 0.1 * rng.standard_normal(D)]).astype(np.float32)
     if rope is not None:
-        s.rope = O.rope_table(rope, D, GRID_H, GRID_W, SPECIAL, 100.0)
+        s.rope = O.rope_table(rope, D, grid[0], grid[1], grid[2], 100.0)
         s.rope_layout = rope
     y = rng.standard_normal((batch, tokens, s.ld)).astype(np.float32)
     y[..., :s.width] += 0.5 * rng.standard_normal(s.width).astype(np.float32)  # per-channel offsets
@@ -151,6 +152,45 @@ def test_fused_prepare_equals_the_two_steps(oracle, torch_gpu, case):
     e = oracle.errors(oracle.decode16(gather_rows(o_fused, rows), 0), oracle.decode16(emu16, 0))
     print(f"vs reference arithmetic: {e}")
     assert e["cos"] >= 0.999 and e["max_abs"] <= 2e-2, e
+
+
+ROPE_FRAMES = [(1, 1, 0), (5, 7, 3), (8, 8, 0), (64, 64, 0)]  # (grid_h, grid_w, special): frame_len 1, 38, 64, 4096
+
+
+@pytest.mark.parametrize("frame", ROPE_FRAMES)
+def test_rope_rows_wrap_at_any_frame_length(oracle, torch_gpu, frame):
+    """Token t takes RoPE row t % frame_len (qkv.cu:25,110), which the kernels
+    form by a multiply with a host-computed reciprocal: frame lengths of 1, 38,
+    64 (a power of two) and 4096 (more than the 300 tokens), at both head dims
+    and both layouts, standalone bit for bit against the oracle and fused bit
+    for bit against the two GPU steps."""
+    import spl_sage as S
+    from spl_sage import qkv as Q
+
+    torch = torch_gpu
+    T, B = 300, 2
+    for D, H, rope in ((64, 4, 0), (128, 2, 1)):
+        rng = np.random.default_rng(300 + frame[0] + D)
+        s, y = _spec(oracle, rng, D, H, 0, B, T, 1, rope, True, grid=frame)
+        print(f"frame {frame}: frame_len {s.rope.shape[0]} D{D} H{H} B{B} T{T} rope {rope}", flush=True)
+        inp, qn, rp = _device(torch, s, y)
+        sa = S.SageAttention(None, D)
+        outs = [torch.empty((B, T, H, D), dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+        Q.QkvPrologue(sa).run(inp, T, H, qn, rp, Q.QkvOut(*(S.TensorMut(t) for t in outs)), batch=B)
+        torch.cuda.synchronize()
+        q16, k16, v16 = oracle.qkv_prologue(s, y)
+        for name, got, w in zip("qkv", outs, (q16, k16, v16)):
+            g = from_device16(got)
+            assert np.array_equal(g, w), (name, int((g != w).sum()))
+
+        p = oracle.Problem(B, H, T, D, dtype=0)
+        ws = sa.workspace(S.Shape(B, H, T))
+        out = torch.empty((B, T, H, D), dtype=torch.bfloat16, device="cuda")
+        sa.forward_qkv(ws, inp, S.TensorMut(out), qn, rp)
+        torch.cuda.synchronize()
+        assert_prologue_equal(read_workspace(ws, p), oracle.prologue(p, q16, k16, v16))
+        _, o_two = run(torch, p, q16, k16, v16, want_ws=False)
+        assert np.array_equal(from_device16(out), o_two)
 
 
 def test_refusals_carry_the_references_text(oracle, torch_gpu):
