@@ -134,10 +134,10 @@ __global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(co
     constexpr int KCPR = D / 16;          // chunks per K row
     static_assert(CPT >= 1, "tile too small for 256 threads");
 
-    // K and V are double-buffered separately: step j reads K(j+1) and V(j)
-    // while K(j+2) and V(j+1) arrive, so both rings have period two. Separate
-    // LDS objects let the compiler see that the direct-to-LDS prefetch into
-    // one buffer never aliases the MFMA operand reads of another.
+    // K and V are double-buffered separately: step j reads K(j) and V(j)
+    // while K(j+1) and V(j+1) arrive in the other buffers. Separate LDS
+    // objects let the compiler see that the direct-to-LDS prefetch into one
+    // buffer never aliases the MFMA operand reads of another.
     __shared__ __attribute__((aligned(16))) uint8_t ldsK0[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t ldsK1[TILE];
     __shared__ __attribute__((aligned(16))) uint8_t ldsV0[TILE];
