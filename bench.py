@@ -178,11 +178,15 @@ def cpu_baseline(q, k, v, cfg: int, budget_s: float = 3.0) -> dict:
 
 def vggt_bench(args, torch, S) -> int:
     """The reference's gpu_bench (tests.rs:817-990): VGGT-Omega's global
-    attention at 512x336, B1 H16 D64, `frames` frames of 689 tokens, dense or
-    KV-merged (stride 2 or 4, every frame merged as in vggt_layout), with the
-    PvAccum and QK-norm options. Prints one JSON line: prologue and attention
-    times, attention TOPS over the merged keys (mod.rs:905-910)."""
-    B, H, D, frames = 1, 16, 64, args.frames
+    attention at 512x336, B1, `heads` heads of `head_dim` (16 and 64 by
+    default, SAGE_HEADS / SAGE_D as the reference reads them), `frames` frames
+    of 689 tokens (SAGE_FRAMES), dense or KV-merged (stride 2 or 4, every frame
+    merged as in vggt_layout), with the PvAccum and QK-norm options. With
+    --tiles all (SAGE_TILES=all) it sweeps the reference's tile list under
+    both PvAccum modes (tests.rs:896-915); every tile runs the one CDNA4
+    kernel here. Prints one JSON line: prologue and attention times, attention
+    TOPS over the merged keys (mod.rs:905-910)."""
+    B, H, D, frames = 1, args.heads, args.head_dim, args.frames
     layout = S.FrameLayout(frames, 17, 21, 32, 0)
     N = frames * layout.tokens_per_frame()
     g = torch.Generator(device="cuda").manual_seed(0)
@@ -192,10 +196,16 @@ def vggt_bench(args, torch, S) -> int:
     v = torch.randn((B, N, H, D), generator=g, device="cuda").to(torch.bfloat16)
     out = torch.empty_like(q)
     stream = torch.cuda.current_stream()
-    cfg = S.Config(S.Config.for_head_dim(D).tile, S.PvAccum.F16 if args.pv16 else S.PvAccum.F32)
-    sa = S.SageAttention(stream, D, cfg)
+    base = S.Config.for_head_dim(D).tile
+    tiles = [base]
+    if args.tiles == "all":
+        for t in (S.Tile(4, 2, 2), S.Tile(4, 2, 4), S.Tile(4, 1, 3), S.Tile(8, 1, 3), S.Tile(8, 1, 4)):
+            if t != base and not (D > 64 and t.m_tiles > 1):
+                tiles.append(t)
+        configs = [S.Config(t, pv) for pv in (S.PvAccum.F32, S.PvAccum.F16) for t in tiles]
+    else:
+        configs = [S.Config(base, S.PvAccum.F16 if args.pv16 else S.PvAccum.F32)]
     merge = S.KvMerge.Pool(args.merge, layout) if args.merge > 1 else S.KvMerge.Dense
-    ws = sa.workspace(S.Shape(B, H, N), merge)
     qk_norm = None
     if args.qk_norm:
         lnp = torch.cat([1 + 0.5 * torch.randn(D, generator=g, device="cuda"), 0.8 * torch.randn(D, generator=g, device="cuda"),
@@ -203,27 +213,40 @@ def vggt_bench(args, torch, S) -> int:
         qk_norm = S.QkNorm(lnp.float().contiguous(), 1e-5)
     opts = S.Options(qk_norm=qk_norm)
     qt, kt, vt, ot = S.Tensor(q), S.Tensor(k), S.Tensor(v), S.TensorMut(out)
-    plan = ws.plan()
-    ops = S.flops(plan, D)
-    sa.prepare(ws, qt, kt, vt, opts)
-    for _ in range(args.warmup):
-        sa.attend(ws, ot)
-    torch.cuda.synchronize()
     reps = max(args.steps, 5)
-    attn_ms = time_events(torch, stream, lambda: sa.attend(ws, ot), reps)
-    prep_ms = time_events(torch, stream, lambda: sa.prepare(ws, qt, kt, vt, opts), reps)
-    step_ms = time_events(torch, stream, lambda: sa.forward(ws, qt, kt, vt, ot, opts), reps)
+    rows = []
+    for cfg in configs:
+        sa = S.SageAttention(stream, D, cfg)
+        ws = sa.workspace(S.Shape(B, H, N), merge)
+        plan = ws.plan()
+        ops = S.flops(plan, D)
+        sa.prepare(ws, qt, kt, vt, opts)
+        for _ in range(args.warmup):
+            sa.attend(ws, ot)
+        torch.cuda.synchronize()
+        attn_ms = time_events(torch, stream, lambda: sa.attend(ws, ot), reps)
+        prep_ms = time_events(torch, stream, lambda: sa.prepare(ws, qt, kt, vt, opts), reps)
+        step_ms = time_events(torch, stream, lambda: sa.forward(ws, qt, kt, vt, ot, opts), reps)
+        attn_tops = ops / (attn_ms * 1e-3) / 1e12
+        t = cfg.tile
+        rows.append({"tile": f"{t.warps}w{t.m_tiles}m{t.stages}s", "pv_accum": cfg.pv_accum.name,
+                     "prologue_ms": round(prep_ms, 4), "attention_ms": round(attn_ms, 4),
+                     "attention_tops": round(attn_tops, 1),
+                     "attention_frac_of_peak": round(attn_tops / VENDOR_PEAK_TOPS, 4), "step_ms": round(step_ms, 4),
+                     "step_tops": round(ops / (step_ms * 1e-3) / 1e12, 1)})
+        del ws
     regs, spill = sa.attn_resources()
     mode = ("dense" if args.merge == 1 else f"merge{args.merge}") + ("_pv16" if args.pv16 else "") + \
         ("_qknorm" if args.qk_norm else "")
-    attn_tops = ops / (attn_ms * 1e-3) / 1e12
-    print(json.dumps({
-        "workload": "VGGT-Omega global attention (reference gpu_bench)", "mode": mode, "frames": frames,
-        "heads": H, "head_dim": D, "tokens": N, "keys": plan.tk, "prologue_ms": round(prep_ms, 4),
-        "attention_ms": round(attn_ms, 4), "attention_tops": round(attn_tops, 1),
-        "attention_frac_of_peak": round(attn_tops / VENDOR_PEAK_TOPS, 4), "step_ms": round(step_ms, 4),
-        "step_tops": round(ops / (step_ms * 1e-3) / 1e12, 1), "vgprs_dense_kernel": regs, "spill": spill,
-    }), flush=True)
+    line = {"workload": "VGGT-Omega global attention (reference gpu_bench)", "mode": mode, "frames": frames,
+            "heads": H, "head_dim": D, "tokens": N, "keys": plan.tk}
+    if args.tiles == "all":
+        line["mode"] = mode.replace("_pv16", "")
+        line["configs"] = rows
+    else:
+        line.update({k: v for k, v in rows[0].items() if k not in ("tile", "pv_accum")})
+    line.update({"vgprs_dense_kernel": regs, "spill": spill})
+    print(json.dumps(line), flush=True)
     return 0
 
 
@@ -316,8 +339,15 @@ def main() -> int:
     ap.add_argument("--no-peak", action="store_true", help="skip the MFMA peak probes")
     ap.add_argument("--vggt", action="store_true",
                     help="instead of the headline line: the reference's gpu_bench workload (tests.rs:817-990), "
-                         "VGGT-Omega global attention, 689-token frames (17 special + 21x32 patches), 16 heads of 64")
-    ap.add_argument("--frames", type=int, default=200, help="--vggt: frames (200 = 137800 tokens)")
+                         "VGGT-Omega global attention, 689-token frames (17 special + 21x32 patches), by default 16 heads of 64")
+    ap.add_argument("--frames", type=int, default=int(os.environ.get("SAGE_FRAMES", 200)),
+                    help="--vggt: frames (200 = 137800 tokens; default $SAGE_FRAMES or 200)")
+    ap.add_argument("--heads", type=int, default=int(os.environ.get("SAGE_HEADS", 16)),
+                    help="--vggt: heads (default $SAGE_HEADS or 16)")
+    ap.add_argument("--head-dim", type=int, default=int(os.environ.get("SAGE_D", 64)), choices=[64, 128],
+                    help="--vggt: head dim (default $SAGE_D or 64)")
+    ap.add_argument("--tiles", choices=["base", "all"], default="all" if os.environ.get("SAGE_TILES") == "all" else "base",
+                    help="--vggt: 'all' sweeps the reference's tile list under both PvAccum modes (SAGE_TILES=all)")
     ap.add_argument("--merge", type=int, default=1, choices=[1, 2, 4], help="--vggt: KV merge stride (1 = dense)")
     ap.add_argument("--pv16", action="store_true", help="--vggt: PvAccum::F16")
     ap.add_argument("--qk-norm", action="store_true", help="--vggt: fused QK LayerNorm")
