@@ -250,6 +250,123 @@ def vggt_bench(args, torch, S) -> int:
     return 0
 
 
+def _time_ms(torch, stream, fn, reps: int):
+    """time_ms (tests.rs:733-748): one warm-up call, then (median, best) of
+    `reps` individually event-timed calls."""
+    fn()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    evs[-1][1].synchronize()
+    t = sorted(a.elapsed_time(b) for a, b in evs)
+    return t[len(t) // 2], t[0]
+
+
+def gpu_bench(args, torch, S) -> int:
+    """The reference's gpu_bench (tests.rs:817-1022) with its file protocol, so
+    its torch_ref.py gen / compare run around this library unchanged: with
+    SAGE_RUN=DIR it reads DIR/meta.txt (frames, heads, head_dim, special,
+    grid_h, grid_w) and bf16 [T][H][D] q.bin, k.bin, v.bin, and writes
+    out_<mode>.bin (out_<mode>_pv16.bin for PvAccum::F16) of the base tile
+    there; otherwise it times random inputs of SAGE_FRAMES VGGT frames,
+    SAGE_HEADS heads of SAGE_D. Every config (the base tile, or the
+    reference's list with SAGE_TILES=all, under both PvAccum modes) runs
+    dense, merge2 and merge4, one JSON line each with the reference's keys;
+    the lines and the MFMA peaks go to $SAGE_OUT/bench_d<D>_f<frames>.json.
+    SAGE_VARIANTS (NVRTC defines of the reference's CUDA source) has no
+    counterpart: the kernels here are compiled ahead of time."""
+    import numpy as np
+
+    run_dir = os.environ.get("SAGE_RUN")
+    if run_dir:
+        meta = {}
+        with open(os.path.join(run_dir, "meta.txt")) as f:
+            for ln in f:
+                if "=" in ln:
+                    k_, v_ = ln.split("=", 1)
+                    meta[k_.strip()] = v_.strip()
+        layout = S.FrameLayout(int(meta["frames"]), int(meta["special"]), int(meta["grid_h"]), int(meta["grid_w"]), 0)
+        heads, d = int(meta["heads"]), int(meta["head_dim"])
+    else:
+        layout = S.FrameLayout(args.frames, 17, 21, 32, 0)
+        heads, d = args.heads, args.head_dim
+    frames = layout.frames
+    T = frames * layout.tokens_per_frame()
+    n = T * heads * d
+    shape = S.Shape(1, heads, T)
+    t0 = time.perf_counter()
+    if run_dir:
+        def load(name):
+            raw = np.fromfile(os.path.join(run_dir, name), dtype="<u2")
+            if raw.size < n:
+                raise SystemExit(f"{name}: input files too small ({raw.size} < {n} elements)")
+            return torch.from_numpy(raw[:n].view(np.int16).reshape(T, heads, d)).cuda().view(torch.bfloat16)
+        q, k, v = load("q.bin"), load("k.bin"), load("v.bin")
+    else:
+        # Timing does not depend on the values (tests.rs:875-880).
+        g = torch.Generator(device="cuda").manual_seed(1)
+        q, k, v = ((torch.randn((T, heads, d), generator=g, device="cuda") * 1.5).to(torch.bfloat16) for _ in range(3))
+    q, k, v = (x.unsqueeze(0) for x in (q, k, v))
+    print(f"inputs ready in {time.perf_counter() - t0:.1f} s", flush=True)
+    stream = torch.cuda.current_stream()
+    probe = S.SageAttention(stream, d)
+    peaks = {}
+    for name, which in (("sg_peak_s8", 0), ("sg_peak_e4m3_f32", 1), ("sg_peak_bf16_f32", 2)):
+        peaks[name] = probe.peak(which)
+        print(f"peak {name}: {peaks[name]:.1f} TOPS", flush=True)
+    base = S.Config.for_head_dim(d).tile
+    tiles = [base]
+    if os.environ.get("SAGE_TILES") == "all" or args.tiles == "all":
+        for t in (S.Tile(4, 2, 2), S.Tile(4, 2, 4), S.Tile(4, 1, 3), S.Tile(8, 1, 3), S.Tile(8, 1, 4)):
+            if t != base and not (d > 64 and t.m_tiles > 1):
+                tiles.append(t)
+    if os.environ.get("SAGE_VARIANTS"):
+        print("SAGE_VARIANTS: kernel-source defines do not apply to this build; each config runs once", flush=True)
+    out = torch.zeros((1, T, heads, d), dtype=torch.bfloat16, device="cuda")
+    qt, kt, vt, ot = S.Tensor(q), S.Tensor(k), S.Tensor(v), S.TensorMut(out)
+    dense_plan = S.Plan.new(shape, S.KvMerge.Dense)
+    lines = []
+    for pv in (S.PvAccum.F32, S.PvAccum.F16):
+        for tile in tiles:
+            sa = S.SageAttention(stream, d, S.Config(tile, pv))
+            regs, spill = sa.attn_resources()
+            for mode, merge in (("dense", S.KvMerge.Dense), ("merge2", S.KvMerge.Pool(2, layout)),
+                                ("merge4", S.KvMerge.Pool(4, layout))):
+                ws = sa.workspace(shape, merge)
+                opts = S.Options()
+                prep = lambda: sa.prepare(ws, qt, kt, vt, opts)
+                prep_ms, _ = _time_ms(torch, stream, prep, 5)
+                attn_ms, attn_best = _time_ms(torch, stream, lambda: sa.attend(ws, ot), 3 if mode == "dense" else 5)
+                plan = ws.plan()
+                tops = S.flops(plan, d) / (attn_ms * 1e-3) / 1e12
+                dense_tops = S.flops(dense_plan, d) / ((attn_ms + prep_ms) * 1e-3) / 1e12
+                line = {"tile": f"{tile.warps}w{tile.m_tiles}m{tile.stages}s", "variant": "",
+                        "pv_accum": "f32" if pv == S.PvAccum.F32 else "f16", "regs": regs, "spill": spill,
+                        "mode": mode, "frames": frames, "heads": heads, "head_dim": d, "tokens": T, "keys": plan.tk,
+                        "prep_ms": round(prep_ms, 3), "attn_ms": round(attn_ms, 3), "attn_best_ms": round(attn_best, 3),
+                        "attn_tops": round(tops, 1), "dense_equiv_tops": round(dense_tops, 1),
+                        "workspace_mb": round(ws.bytes() / 1e6, 1)}
+                print(json.dumps(line), flush=True)
+                lines.append(line)
+                if run_dir and tile == base:
+                    prep()
+                    sa.attend(ws, ot)
+                    torch.cuda.synchronize()
+                    suffix = "_pv16" if pv == S.PvAccum.F16 else ""
+                    out.view(torch.int16).cpu().numpy().astype("<i2").tofile(
+                        os.path.join(run_dir, f"out_{mode}{suffix}.bin"))
+                del ws
+    out_dir = os.environ.get("SAGE_OUT", "/out/sage")
+    os.makedirs(out_dir, exist_ok=True)
+    path = os.path.join(out_dir, f"bench_d{d}_f{frames}.json")
+    with open(path, "w") as f:
+        f.write(json.dumps({"peaks_tops": {k_: round(v_, 1) for k_, v_ in peaks.items()}, "runs": lines}) + "\n")
+    print(f"wrote {path}", flush=True)
+    return 0
+
+
 def qkv_bench(args, torch, S) -> int:
     """The upstream QKV prologue (qkv.rs, qkv.cu) in front of the chosen
     configuration: the fused projection y (bf16 [B][N][(H + 2 HKV) * D]) with
@@ -351,6 +468,9 @@ def main() -> int:
     ap.add_argument("--merge", type=int, default=1, choices=[1, 2, 4], help="--vggt: KV merge stride (1 = dense)")
     ap.add_argument("--pv16", action="store_true", help="--vggt: PvAccum::F16")
     ap.add_argument("--qk-norm", action="store_true", help="--vggt: fused QK LayerNorm")
+    ap.add_argument("--gpu-bench", action="store_true",
+                    help="the reference's gpu_bench with its file protocol (SAGE_RUN, SAGE_OUT, SAGE_FRAMES, "
+                         "SAGE_HEADS, SAGE_D, SAGE_TILES): dense, merge2 and merge4 for every config")
     ap.add_argument("--qkv", action="store_true",
                     help="instead of the headline line: the upstream QKV prologue in front of --config, the "
                          "reference's two steps against the fused prepare_qkv")
@@ -369,6 +489,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.vggt:
         return vggt_bench(args, torch, S)
+    if args.gpu_bench:
+        return gpu_bench(args, torch, S)
     if args.qkv:
         return qkv_bench(args, torch, S)
     if args.only == "copy":
