@@ -5,8 +5,11 @@
 // 405-440). No GPU call is made. Exit status 0 when every check passes.
 #include <cmath>
 #include <cstdio>
+#include <atomic>
 #include <string>
+#include <thread>
 #include <type_traits>
+#include <vector>
 
 #include "spl_sage.hpp"
 #include "spl_sage_sched.hpp"
@@ -50,6 +53,35 @@ static void engine_handles_are_move_only() {
     static_assert(std::is_nothrow_move_constructible<SageAttention>::value, "");
     static_assert(!std::is_copy_constructible<Workspace>::value, "");
     static_assert(std::is_nothrow_move_constructible<Workspace>::value, "");
+}
+
+// tests.rs:17-22 asks for an engine that is Send + Sync. The C ABI's state
+// shared across threads is its error channel: eight threads refuse their own
+// shapes concurrently, and each reads back its own text.
+static void error_text_is_per_thread() {
+    std::atomic<int> wrong{0};
+    std::vector<std::thread> pool;
+    for (int t = 0; t < 8; t++)
+        pool.emplace_back([t, &wrong] {
+            sage_kv_merge dense{};
+            dense.stride = 1;
+            for (int i = 0; i < 2000; i++) {
+                sage_shape s{};
+                s.batch = 1;
+                s.heads = 6 + t;
+                s.kv_heads = 4;  // divides 6 + t only at t = 2 and t = 6
+                s.tokens = 100;
+                sage_plan p;
+                const sage_status st = sage_plan_new(&s, &dense, &p);
+                const bool refused = (6 + t) % 4 != 0;
+                const std::string want = std::to_string(6 + t) + " query heads are not a multiple of 4 KV heads";
+                if (refused ? (st != SAGE_ERR_INVALID || sage_last_error() != want)
+                            : (st != SAGE_OK || sage_last_error()[0] != 0))
+                    wrong++;
+            }
+        });
+    for (auto& th : pool) th.join();
+    CHECK(wrong.load() == 0);
 }
 
 // tests.rs:95-110: 689 dense keys + 2 x (17 + 6 x 8) pooled.
@@ -250,6 +282,7 @@ int main() {
         void (*fn)();
     } tests[] = {
         {"engine_handles_are_move_only", engine_handles_are_move_only},
+        {"error_text_is_per_thread", error_text_is_per_thread},
         {"dense_first_frame_keeps_its_keys", dense_first_frame_keeps_its_keys},
         {"vggt_merge_geometry", vggt_merge_geometry},
         {"plan_rejects_bad_layouts", plan_rejects_bad_layouts},
