@@ -118,9 +118,10 @@ __device__ __forceinline__ bool half_selector(int lane) {
     return (int)__builtin_amdgcn_permlane32_swap(lane, lane, false, false)[0] != lane;
 }
 
-// The merged head-dim-128 kernel needs the registers of two waves a SIMD.
+// Workgroups a CU: four at head dim 64 (<= 128 VGPRs), three at head dim 128
+// (<= 168); the merged head-dim-128 kernel needs the registers of two.
 template <int D, bool CAUSAL, bool MERGE>
-__global__ __launch_bounds__(256, (MERGE && D == 128) ? 2 : 3) void sage_attn(const int8_t* __restrict__ q8, const float* __restrict__ q_scale,
+__global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(const int8_t* __restrict__ q8, const float* __restrict__ q_scale,
                                                     const int8_t* __restrict__ k8,
                                                     const float* __restrict__ k_scale,
                                                     const uint8_t* __restrict__ v8, const float* __restrict__ stats,
@@ -508,28 +509,11 @@ static hipError_t launch_d(const AttendBufs& w, const Geom& g, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Dense, causal (an extension) or merged (sg_attn_merge); the API refuses
-// causal masking over merged keys.
-template <int D>
-static hipError_t launch_dim(const AttendBufs& w, const Geom& g, hipStream_t s) {
-    if (g.merge > 1) return launch_d<D, false, true>(w, g, s);
-    return (g.flags & F_CAUSAL) ? launch_d<D, true, false>(w, g, s) : launch_d<D, false, false>(w, g, s);
-}
-
-hipError_t launch_attention(int head_dim, const AttendBufs& w, const Geom& g, hipStream_t s) {
-    return head_dim == 64 ? launch_dim<64>(w, g, s) : launch_dim<128>(w, g, s);
-}
-
-template <int D>
-static const void* attention_kernel(bool causal, bool merge) {
-    if (merge) return reinterpret_cast<const void*>(&sage_attn<D, false, true>);
-    return causal ? reinterpret_cast<const void*>(&sage_attn<D, true, false>)
-                  : reinterpret_cast<const void*>(&sage_attn<D, false, false>);
-}
-
-hipError_t attention_resources(int head_dim, bool causal, bool merge, int* regs, int* spill, int* lds) {
+template <bool CAUSAL, bool MERGE>
+static hipError_t resources_of(int head_dim, int* regs, int* spill, int* lds) {
     hipFuncAttributes a;
-    const void* f = head_dim == 64 ? attention_kernel<64>(causal, merge) : attention_kernel<128>(causal, merge);
+    const void* f = head_dim == 64 ? reinterpret_cast<const void*>(&sage_attn<64, CAUSAL, MERGE>)
+                                   : reinterpret_cast<const void*>(&sage_attn<128, CAUSAL, MERGE>);
     hipError_t e = hipFuncGetAttributes(&a, f);
     if (e != hipSuccess) return e;
     *regs = a.numRegs;
@@ -537,5 +521,39 @@ hipError_t attention_resources(int head_dim, bool causal, bool merge, int* regs,
     *lds = (int)a.sharedSizeBytes;
     return hipSuccess;
 }
+
+// This file is compiled twice. The dense and causal kernels (this pass) take
+// LLVM's iterative occupancy-keeping pre-RA scheduler and a bottom-up post-RA
+// pass, which reorder their instructions only (outputs bit-identical) and are
+// faster for them; the merged kernels (SAGE_ATTN_MERGED) are faster with the
+// default order and are built in the second pass.
+#ifndef SAGE_ATTN_MERGED
+
+// Dense, causal (an extension) or merged (sg_attn_merge); the API refuses
+// causal masking over merged keys.
+hipError_t launch_attention(int head_dim, const AttendBufs& w, const Geom& g, hipStream_t s) {
+    if (g.merge > 1) return launch_attention_merged(head_dim, w, g, s);
+    if (head_dim == 64)
+        return (g.flags & F_CAUSAL) ? launch_d<64, true, false>(w, g, s) : launch_d<64, false, false>(w, g, s);
+    return (g.flags & F_CAUSAL) ? launch_d<128, true, false>(w, g, s) : launch_d<128, false, false>(w, g, s);
+}
+
+hipError_t attention_resources(int head_dim, bool causal, bool merge, int* regs, int* spill, int* lds) {
+    if (merge) return attention_resources_merged(head_dim, regs, spill, lds);
+    return causal ? resources_of<true, false>(head_dim, regs, spill, lds)
+                  : resources_of<false, false>(head_dim, regs, spill, lds);
+}
+
+#else
+
+hipError_t launch_attention_merged(int head_dim, const AttendBufs& w, const Geom& g, hipStream_t s) {
+    return head_dim == 64 ? launch_d<64, false, true>(w, g, s) : launch_d<128, false, true>(w, g, s);
+}
+
+hipError_t attention_resources_merged(int head_dim, int* regs, int* spill, int* lds) {
+    return resources_of<false, true>(head_dim, regs, spill, lds);
+}
+
+#endif
 
 }  // namespace sage

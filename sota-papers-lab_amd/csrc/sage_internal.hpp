@@ -60,10 +60,14 @@ hipError_t launch_qkv(int head_dim, const uint16_t* y, const QkvOutDev& o, const
 constexpr int ATTN_ROWS = 128;
 
 hipError_t launch_attention(int head_dim, const AttendBufs& w, const Geom& g, hipStream_t s);
+// The merged kernels' launch, from the second compilation of the attention
+// source (launch_attention calls it for merged plans).
+hipError_t launch_attention_merged(int head_dim, const AttendBufs& w, const Geom& g, hipStream_t s);
 
 // Kernel resources (VGPRs, scratch, LDS) of the attention kernel for
 // head_dim: dense, causal or KV-merged.
 hipError_t attention_resources(int head_dim, bool causal, bool merge, int* regs, int* spill, int* lds);
+hipError_t attention_resources_merged(int head_dim, int* regs, int* spill, int* lds);
 
 // MFMA peak probe: which 0 = INT8, 1 = FP8, 2 = BF16; returns dense TOPS.
 hipError_t run_peak(int which, int iters, hipStream_t s, double* tops);
