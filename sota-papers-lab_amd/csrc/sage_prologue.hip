@@ -451,7 +451,9 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
             if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                kv[i][e] = ok ? (fk[e] + 0.0f) - mk[e] : 0.f;
+                // The reference's (k + 0) - mean differs from k - mean only in
+                // the sign of a zero, which neither |kv| nor its INT8 code keeps.
+                kv[i][e] = ok ? fk[e] - mk[e] : 0.f;
                 amax = fmaxf(amax, fabsf(kv[i][e]));
             }
         }
@@ -476,8 +478,11 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
             float vq[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                // The reference sums the (one) member from 0.0f first: -0 becomes +0.
-                kv[i][e] = ok ? (fk[e] + 0.0f) - mk[e] : 0.f;
+                // The reference sums the (one) member from 0.0f first, so -0
+                // becomes +0: that matters for V's E4M3 code (0x80 against
+                // 0x00) but not for K, whose |kv| and INT8 code drop the sign
+                // of a zero.
+                kv[i][e] = ok ? fk[e] - mk[e] : 0.f;
                 amax = fmaxf(amax, fabsf(kv[i][e]));
                 vq[e] = ok ? ((fv[e] + 0.0f) - mv[e]) * iv[e] : 0.f;
             }
