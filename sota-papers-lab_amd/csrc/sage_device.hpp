@@ -319,8 +319,6 @@ struct QkvOutDev {
     int v_f16;
 };
 
-// x rounded to the nearest bf16 (ties to even), as a float.
-__device__ __forceinline__ float round_bf16(float x) { return __uint_as_float(pack_bf16x2(x, 0.f) << 16); }
 
 // Byte position of key k (0..63) of a 64-key block inside each channel row of
 // the V tile. The 32x32 INT8 MFMA leaves key 32t + 8j + 4g + r of a column

@@ -97,8 +97,14 @@ template <int D>
 __device__ __forceinline__ void qkv_row(float* x, const QkvDev& qa, const QkvLane& L, const QkvTok& T, int part,
                                         int ch) {
     qkv_apply<D>(x, qa, L, T, part, ch);
+    // Pairs through one packed conversion: the low bf16 back to f32 by a
+    // shift, the high one by a mask.
 #pragma unroll
-    for (int e = 0; e < 8; e++) x[e] = round_bf16(x[e]);
+    for (int e = 0; e < 8; e += 2) {
+        const uint32_t u = pack_bf16x2(x[e], x[e + 1]);
+        x[e] = __uint_as_float(u << 16);
+        x[e + 1] = __uint_as_float(u & 0xffff0000u);
+    }
 }
 
 // sage_quant.cu:59-160 (sg_prep), in two roles. Under QK LayerNorm (LN, the
