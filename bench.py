@@ -377,7 +377,19 @@ def qkv_bench(args, torch, S) -> int:
     or re-reads Q, K and V in bf16. Prints one JSON line."""
     from spl_sage import qkv as Q
 
-    B, H, HK, N, D, dt, causal, *_ = CONFIGS[args.config]
+    merge = S.KvMerge.Dense
+    if args.vggt:
+        # The reference caller's layer (vggt/trunk): `frames` frames of 17 special
+        # tokens and a 21 x 32 patch grid, 16 heads of 64, the frame-relative VGGT
+        # RoPE table, dense or KV-merged keys.
+        layout = S.FrameLayout(args.frames, 17, 21, 32, 0)
+        B, H, HK, N, D, causal = 1, args.heads, args.heads, args.frames * layout.tokens_per_frame(), args.head_dim, False
+        if args.merge > 1:
+            merge = S.KvMerge.Pool(args.merge, layout)
+        name = (f"VGGT {args.frames} frames H{H} D{D} bf16" + ("" if args.merge == 1 else f" merge{args.merge}"))
+    else:
+        B, H, HK, N, D, dt, causal, *_ = CONFIGS[args.config]
+        name = NAMES[args.config]
     g = torch.Generator(device="cuda").manual_seed(0)
     width = (H + 2 * HK) * D
     y = (torch.randn((B, N, width), generator=g, device="cuda")
@@ -388,14 +400,17 @@ def qkv_bench(args, torch, S) -> int:
           (0.1 * torch.randn((D,), generator=g, device="cuda")).float(),
           (1 + 0.2 * torch.randn((D,), generator=g, device="cuda")).float(),
           (0.1 * torch.randn((D,), generator=g, device="cuda")).float()]
-    gw = 64
-    table = Q.RopeTable.vggt((N + gw - 1) // gw, gw, 0, 100.0, D)
+    if args.vggt:
+        table = Q.RopeTable.vggt(21, 32, 17, 100.0, D)
+    else:
+        gw = 64
+        table = Q.RopeTable.vggt((N + gw - 1) // gw, gw, 0, 100.0, D)
     rope = Q.Rope(table.upload(), Q.RopeLayout.Vggt, table.frame_len)
     norm = Q.QkNorm(Q.NormKind.LayerNorm, nw[0], nw[2], nw[1], nw[3], 1e-6)
     inp = Q.QkvIn(y, width, chan=chan, bias=bias)
     stream = torch.cuda.current_stream()
     sa = S.SageAttention(stream, D)
-    ws = sa.workspace(S.Shape(B, H, N, HK if HK != H else 0))
+    ws = sa.workspace(S.Shape(B, H, N, HK if HK != H else 0), merge)
     out = torch.empty((B, N, H, D), dtype=torch.bfloat16, device="cuda")
     q = torch.empty((B, N, H, D), dtype=torch.bfloat16, device="cuda")
     k = torch.empty((B, N, HK, D), dtype=torch.bfloat16, device="cuda")
@@ -434,7 +449,7 @@ def qkv_bench(args, torch, S) -> int:
     ops = S.flops(ws.plan(), D, causal)
     y_bytes = B * N * width * 2
     print(json.dumps({
-        "workload": f"QKV prologue + sage, {NAMES[args.config]} (LayerNorm QK-norm, VGGT RoPE, channel scales, bias)",
+        "workload": f"QKV prologue + sage, {name} (LayerNorm QK-norm, VGGT RoPE, channel scales, bias)",
         "two_step_ms": round(t2, 4), "fused_ms": round(t1, 4), "speedup": round(t2 / t1, 3),
         "qkv_prologue_ms": round(tq, 4), "prepare_from_bf16_ms": round(tpp, 4), "prepare_qkv_ms": round(tpf, 4),
         "qkv_prologue_gbs": round(2 * y_bytes / (tq * 1e-3) / 1e9, 1),
@@ -472,8 +487,9 @@ def main() -> int:
                     help="the reference's gpu_bench with its file protocol (SAGE_RUN, SAGE_OUT, SAGE_FRAMES, "
                          "SAGE_HEADS, SAGE_D, SAGE_TILES): dense, merge2 and merge4 for every config")
     ap.add_argument("--qkv", action="store_true",
-                    help="instead of the headline line: the upstream QKV prologue in front of --config, the "
-                         "reference's two steps against the fused prepare_qkv")
+                    help="instead of the headline line: the upstream QKV prologue in front of --config (or, with "
+                         "--vggt, of the VGGT layer: --frames, --heads, --head-dim, --merge), the reference's two "
+                         "steps against the fused prepare_qkv")
     ap.add_argument("--only", choices=["attend", "prepare", "copy"],
                     help="profiling mode: run only this kernel group --steps times and print its timing "
                          "(copy: a plain 512 MiB device copy, the reference for HBM byte counters)")
@@ -487,12 +503,12 @@ def main() -> int:
     import spl_sage as S
 
     torch.cuda.set_device(0)
+    if args.qkv:
+        return qkv_bench(args, torch, S)
     if args.vggt:
         return vggt_bench(args, torch, S)
     if args.gpu_bench:
         return gpu_bench(args, torch, S)
-    if args.qkv:
-        return qkv_bench(args, torch, S)
     if args.only == "copy":
         n = 512 << 20
         src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
