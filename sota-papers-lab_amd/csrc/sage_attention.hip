@@ -146,6 +146,9 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
     // Merge biases of the current and the next block.
     __shared__ __attribute__((aligned(16))) float ldsB0[MERGE ? BN : 4];
     __shared__ __attribute__((aligned(16))) float ldsB1[MERGE ? BN : 4];
+    // Merged: each wave's per-key logit offsets bias - 1.5 * 2^23 * scl of the
+    // current block, for each of the two Q-scale groups of its 32 queries.
+    __shared__ __attribute__((aligned(16))) float ldsC[MERGE ? 4 * 2 * BN : 4];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, col = lane & 31, half = lane >> 5;
     const int ntq = gridDim.x;
@@ -177,6 +180,9 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
         for (int s = 0; s < KS; s++) qa[s] = *reinterpret_cast<const v4i*>(qrow + 32 * s);
     }
     const float qs = q_scale[bh * (g.tq_pad / QGROUP) + (qi >> 4)];
+    // The Q scales of the wave's two 16-query groups (wave-uniform).
+    const float qsg0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qs), 0));
+    const float qsg1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qs), QGROUP));
     // Consume the Q loads here, before the first barrier: otherwise the
     // compiler sinks them into the key loop and waits for every outstanding
     // load there, prefetches included.
@@ -301,19 +307,32 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
         const float scl = fmaxf(qs * ksc[blk], 1.0e-30f);
         const float xoff = -MAGIC * scl;
         if constexpr (MERGE) {
+            // The logit fmaf(1.5 * 2^23 + S, scl, fmaf(-1.5 * 2^23, scl, bias)):
+            // the inner term depends only on the key and the query group, so
+            // lane l forms it once for key l and both groups (the same value,
+            // bit for bit, that each lane of the group would form) and the
+            // wave reads it back from LDS in place of the bias. A wave's LDS
+            // operations run in order, so the previous block's reads are done.
+            float* cw = ldsC + wv * 2 * BN;
+            {
+                const float bl = bias[lane];
+                cw[lane] = fmaf(-MAGIC, fmaxf(qsg0 * ksc[blk], 1.0e-30f), bl);
+                cw[BN + lane] = fmaf(-MAGIC, fmaxf(qsg1 * ksc[blk], 1.0e-30f), bl);
+            }
+            const float* cg = cw + (col >> 4) * BN;
             // Element (t, r) is key 32t + 8(r >> 2) + 4 half + (r & 3): four
-            // consecutive keys a 16-byte bias read.
+            // consecutive keys a 16-byte read.
             float x[32];
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const float4 bb = *reinterpret_cast<const float4*>(bias + 32 * t + 8 * j + 4 * half);
-                    const float bv[4] = {bb.x, bb.y, bb.z, bb.w};
+                    const float4 cc = *reinterpret_cast<const float4*>(cg + 32 * t + 8 * j + 4 * half);
+                    const float cv[4] = {cc.x, cc.y, cc.z, cc.w};
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const int r = 4 * j + i;
-                        x[16 * t + r] = fmaf(__int_as_float(sc[t][r]), scl, fmaf(-MAGIC, scl, bv[i]));
+                        x[16 * t + r] = fmaf(__int_as_float(sc[t][r]), scl, cv[i]);
                     }
                 }
             float mx = x[0];
@@ -472,7 +491,7 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
     // out = O / l * v_scale + v_mean; lane holds channels 32dt + 8j + 4*half + 0..3.
     const float lt = l + swap_halves(l, sel);
     const float inv = 1.0f / lt;
-    const int ln_e = D == 128 ? lane_now() : lane, half_e = ln_e >> 5, qi_e = q0 + (ln_e & 31);
+    const int ln_e = (D == 128 || MERGE) ? lane_now() : lane, half_e = ln_e >> 5, qi_e = q0 + (ln_e & 31);
     if (qi_e < g.tokens) {
         const float* vmean = stats + bhk * 4 * D + D;
         const float* vscale = vmean + D;
