@@ -220,6 +220,21 @@ static void run_case(const Case& c) {
     p.pv16 = c.pv16 ? 1 : 0;
     const uint16_t* hp = packed.data();
     if (!check_forward(p, ws, hp, hp + hd, hp + 2 * hd, dout.p, scale, !c.merge.is_dense())) failures++;
+
+    // The no-allocation entry point (no reference counterpart) on the same
+    // inputs: the output equals forward's bit for bit.
+    DeviceBuf<uint16_t> dout2(dout.n);
+    sage.forward_noalloc(shape, Tensor{dqkv.p, len, st}, Tensor{dqkv.p + hd, len - hd, st},
+                         Tensor{dqkv.p + 2 * hd, len - 2 * hd, st}, TensorMut{dout2.p, dout2.n, Strides::bthd(T, H, d)},
+                         opts, c.merge);
+    hip_ok(hipDeviceSynchronize(), "forward_noalloc");
+    std::vector<uint16_t> o1(dout.n), o2(dout.n);
+    hip_ok(hipMemcpy(o1.data(), dout.p, o1.size() * 2, hipMemcpyDeviceToHost), "download out");
+    hip_ok(hipMemcpy(o2.data(), dout2.p, o2.size() * 2, hipMemcpyDeviceToHost), "download out2");
+    const bool same = o1 == o2;
+    std::printf("    forward_noalloc %s\n", same ? "equals forward" : "DIFFERS from forward");
+    std::fflush(stdout);
+    if (!same) failures++;
 }
 
 // QkvPrologue::run through the C++ qkv mirror (the reference's
