@@ -58,15 +58,31 @@ constexpr float MAGIC = 12582912.0f;        // 1.5 * 2^23
 constexpr int NEG_INF_BITS = (int)0xFF800000;  // -inf: below every biased score as an int
 constexpr float LOG2_448 = 8.807354922057604f;  // P = 448 for the row max: E4M3's largest finite
 
-// Value of lane ^ 32 (the other half of the wave) with one v_permlane32_swap.
-// The swap returns both operands' new values; in each half of the wave one of
-// the two holds the partner's value. `first` (from half_selector) says which.
-__device__ __forceinline__ int swap_halves(int x, bool first) {
+// A row statistic held in lane l and its partner lane l ^ 32 (the other half
+// of the wave), combined in every lane with one v_permlane32_swap of two copies
+// of x: the swap's first result holds the lower half's values in both halves,
+// its second the upper half's, so every lane combines the same pair in the
+// same order.
+__device__ __forceinline__ int max_halves(int x) {
     const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-    return first ? (int)r[0] : (int)r[1];
+    return max((int)r[0], (int)r[1]);
 }
-__device__ __forceinline__ float swap_halves(float x, bool first) {
-    return __int_as_float(swap_halves(__float_as_int(x), first));
+__device__ __forceinline__ float fmax_halves(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    // v_med3_f32 with FLT_MAX: the maximum of two non-NaN values without the
+    // canonicalising v_max_f32 that fmaxf puts on each swapped register.
+    return __builtin_amdgcn_fmed3f(__int_as_float((int)r[0]), __int_as_float((int)r[1]), 3.4028234663852886e38f);
+}
+__device__ __forceinline__ float sum_halves(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+    return __int_as_float((int)r[0]) + __int_as_float((int)r[1]);
+}
+// max(m, x) for the running max: v_med3_f32(m, x, FLT_MAX) in one instruction
+// (fmaxf on the loop-carried m costs a canonicalising v_max_f32 m, m every
+// block). Neither operand is a NaN: m starts at -1e30 and x is a finite logit
+// or -inf.
+__device__ __forceinline__ float running_max(float m, float x) {
+    return __builtin_amdgcn_fmed3f(m, x, 3.4028234663852886e38f);
 }
 // Values the compiler may not re-derive or rematerialise: a uniform pointer
 // stays in SGPRs and is not reassociated with per-lane offsets; a VGPR value
@@ -112,10 +128,6 @@ __device__ __forceinline__ bool causal_longest_first(int total, int ntq) {
 // being kept live (or spilled) across the key loop.
 __device__ __forceinline__ int lane_now() {
     return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-}
-
-__device__ __forceinline__ bool half_selector(int lane) {
-    return (int)__builtin_amdgcn_permlane32_swap(lane, lane, false, false)[0] != lane;
 }
 
 // Workgroups a CU: four at head dim 64 (<= 128 VGPRs), three at head dim 128
@@ -170,7 +182,6 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
     const long long bh = (long long)b * g.heads + h, bhk = (long long)b * g.kv_heads + hk;
     const int q0 = qt * ATTN_ROWS + wave * 32;  // first query of this wave
     const int qi = q0 + col;                    // this lane's query
-    const bool sel = half_selector(lane);
 
     // Q^T operand: lane holds channels 32s + 16*half .. +15 of its query.
     v4i qa[KS];
@@ -335,11 +346,18 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
                         x[16 * t + r] = fmaf(__int_as_float(sc[t][r]), scl, cv[i]);
                     }
                 }
-            float mx = x[0];
+            // 16 three-input maxima in a tree (the logits are FMA results, so
+            // fmaxf needs no canonicalising).
+            auto fmax3 = [](float a, float b, float c) __attribute__((always_inline)) {
+                return fmaxf(fmaxf(a, b), c);
+            };
+            float f3[10];
 #pragma unroll
-            for (int e = 1; e < 32; e++) mx = fmaxf(mx, x[e]);
-            mx = fmaxf(mx, swap_halves(mx, sel));
-            const float mnew = fmaxf(m, mx);
+            for (int i = 0; i < 10; i++) f3[i] = fmax3(x[3 * i], x[3 * i + 1], x[3 * i + 2]);
+            float mx = fmaxf(fmax3(fmax3(f3[0], f3[1], f3[2]), fmax3(f3[3], f3[4], f3[5]), fmax3(f3[6], f3[7], f3[8])),
+                             fmax3(f3[9], x[30], x[31]));
+            mx = fmax_halves(mx);
+            const float mnew = running_max(m, mx);
             grow = mnew > m;
             const float alpha = __builtin_amdgcn_exp2f(m - mnew);
             m = mnew;
@@ -379,19 +397,22 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
                     if (32 * t + 8 * (r >> 2) + (r & 3) >= lim) sc[t][r] = NEG_INF_BITS;
         }
         // Row max over this lane's 32 keys (a v_max3 tree), then the partner half.
-        int m3[11];
+        // 32 scores in 16 three-input maxima: 10 over 30 scores, 4 over those
+        // and the last two scores, then 2.
+        auto max3 = [](int a, int b, int c) __attribute__((always_inline)) { return max(max(a, b), c); };
+        int m3[10];
 #pragma unroll
         for (int i = 0; i < 10; i++)
-            m3[i] = max(max(sc[(3 * i) >> 4][(3 * i) & 15], sc[(3 * i + 1) >> 4][(3 * i + 1) & 15]),
-                        sc[(3 * i + 2) >> 4][(3 * i + 2) & 15]);
-        m3[10] = max(sc[1][14], sc[1][15]);
-        int mx = max(max(max(max(m3[0], m3[1]), m3[2]), max(max(m3[3], m3[4]), m3[5])),
-                     max(max(max(m3[6], m3[7]), m3[8]), max(m3[9], m3[10])));
-        mx = max(mx, swap_halves(mx, sel));
+            m3[i] = max3(sc[(3 * i) >> 4][(3 * i) & 15], sc[(3 * i + 1) >> 4][(3 * i + 1) & 15],
+                         sc[(3 * i + 2) >> 4][(3 * i + 2) & 15]);
+        const int m9 = max3(m3[0], m3[1], m3[2]), m10 = max3(m3[3], m3[4], m3[5]);
+        const int m11 = max3(m3[6], m3[7], m3[8]), m12 = max3(m3[9], sc[1][14], sc[1][15]);
+        int mx = max(max3(m9, m10, m11), m12);
+        mx = max_halves(mx);
 
         // The running max in log2 units (a fully masked block gives -inf,
         // which leaves m alone); the row's largest score maps to P = 448.
-        const float mnew = fmaxf(m, fmaf(__int_as_float(mx), scl, xoff));
+        const float mnew = running_max(m, fmaf(__int_as_float(mx), scl, xoff));
         grow = mnew > m;
         const float alpha = __builtin_amdgcn_exp2f(m - mnew);
         m = mnew;
@@ -489,7 +510,7 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
     }
 
     // out = O / l * v_scale + v_mean; lane holds channels 32dt + 8j + 4*half + 0..3.
-    const float lt = l + swap_halves(l, sel);
+    const float lt = sum_halves(l);
     const float inv = 1.0f / lt;
     const int ln_e = (D == 128 || MERGE) ? lane_now() : lane, half_e = ln_e >> 5, qi_e = q0 + (ln_e & 31);
     if (qi_e < g.tokens) {
