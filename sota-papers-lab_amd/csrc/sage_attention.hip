@@ -77,6 +77,16 @@ __device__ __forceinline__ float sum_halves(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
     return __int_as_float((int)r[0]) + __int_as_float((int)r[1]);
 }
+// Floor of the Q and K scales in the attention kernel: 1e-18, whose square is
+// still a normal float.
+constexpr float SCALE_FLOOR = 1.0e-18f;
+constexpr unsigned SCALE_FLOOR_BITS = 0x219392EFu;  // bits of 1e-18f
+// max(k_scale, 1e-18) of a wave-uniform k_scale (>= 0: amax / 127) as an
+// integer max of the bits (non-negative floats order like their bit
+// patterns): one scalar instruction a block instead of a VALU one.
+__device__ __forceinline__ float scale_floor(float s) {
+    return __uint_as_float(max(__float_as_uint(s), SCALE_FLOOR_BITS));
+}
 // max(m, x) for the running max: v_med3_f32(m, x, FLT_MAX) in one instruction
 // (fmaxf on the loop-carried m costs a canonicalising v_max_f32 m, m every
 // block). Neither operand is a NaN: m starts at -1e30 and x is a finite logit
@@ -190,7 +200,11 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
 #pragma unroll
         for (int s = 0; s < KS; s++) qa[s] = *reinterpret_cast<const v4i*>(qrow + 32 * s);
     }
-    const float qs = q_scale[bh * (g.tq_pad / QGROUP) + (qi >> 4)];
+    // The Q scale floored at 1e-18; the K scale gets the same floor in the key
+    // loop (scale_floor), so q_scale * k_scale is a normal float above zero
+    // and a masked -inf score times it stays -inf. Only all-but-zero scales
+    // (amax below about 1e-16) are raised.
+    const float qs = fmaxf(q_scale[bh * (g.tq_pad / QGROUP) + (qi >> 4)], SCALE_FLOOR);
     // The Q scales of the wave's two 16-query groups (wave-uniform).
     const float qsg0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qs), 0));
     const float qsg1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qs), QGROUP));
@@ -314,8 +328,9 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
                        __attribute__((always_inline)) {
         // The reference's fp32 operation order for the logits: no FMA contraction.
 #pragma clang fp contract(off)
-        // q_scale * k_scale, kept above zero so that -inf * scl stays -inf.
-        const float scl = fmaxf(qs * ksc[blk], 1.0e-30f);
+        // q_scale * k_scale, both floored (above), so that -inf * scl stays -inf.
+        const float kscf = scale_floor(ksc[blk]);
+        const float scl = qs * kscf;
         const float xoff = -MAGIC * scl;
         if constexpr (MERGE) {
             // The logit fmaf(1.5 * 2^23 + S, scl, fmaf(-1.5 * 2^23, scl, bias)):
@@ -327,8 +342,8 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
             float* cw = ldsC + wv * 2 * BN;
             {
                 const float bl = bias[lane];
-                cw[lane] = fmaf(-MAGIC, fmaxf(qsg0 * ksc[blk], 1.0e-30f), bl);
-                cw[BN + lane] = fmaf(-MAGIC, fmaxf(qsg1 * ksc[blk], 1.0e-30f), bl);
+                cw[lane] = fmaf(-MAGIC, qsg0 * kscf, bl);
+                cw[BN + lane] = fmaf(-MAGIC, qsg1 * kscf, bl);
             }
             const float* cg = cw + (col >> 4) * BN;
             // Element (t, r) is key 32t + 8(r >> 2) + 4 half + (r & 3): four
