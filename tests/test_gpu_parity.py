@@ -84,6 +84,27 @@ def test_small_cases(oracle, torch_gpu, name):
     _check_attention(oracle, p, want, o, rows, q, k, v, name)
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_zero_scales(oracle, torch_gpu, d):
+    """Degenerate scales: a K head constant over tokens (K smoothing leaves
+    zeros, so every k_scale of that head is 0) and an all-zero 16-row Q group
+    (q_scale 0), causal over a ragged tail. The attention kernel floors both
+    scales before their product multiplies a masked -inf score; the reference
+    arithmetic has no floor, and a zero scale makes every logit of the row 0,
+    so both give uniform attention over the visible keys. Codes bit-exact;
+    outputs finite and at the gate on every row."""
+    p, g = oracle.Problem(1, 3, 333, d, causal=True), oracle.GenSpec(k_off_std=2.0, seed=41)
+    q, k, v = oracle.generate(p, g)
+    k[:, :, 0, :] = k[:, :1, 0, :]
+    q[:, 32:48, 1, :] = 0
+    pro, o = run(torch_gpu, p, q, k, v)
+    want = oracle.prologue(p, q, k, v)
+    assert_prologue_equal(pro, want)
+    assert not want["k_scale"][:, 0].any()  # [batch][kv head][key block]
+    assert not want["q_scale"][:, 1, 2].any()  # [batch][head][16-row group]
+    _check_attention(oracle, p, want, o, np.arange(p.tokens, dtype=np.int32), q, k, v, f"zero scales d{d}")
+
+
 @pytest.mark.parametrize("layout", ["packed", "bhtd"])
 def test_strided_layouts(oracle, torch_gpu, layout):
     p, g = oracle.Problem(2, 3, 389, 64), oracle.GenSpec(k_off_std=2.0, seed=13)
