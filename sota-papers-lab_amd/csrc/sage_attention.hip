@@ -361,8 +361,8 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
                         x[16 * t + r] = fmaf(__int_as_float(sc[t][r]), scl, cv[i]);
                     }
                 }
-            // 16 three-input maxima in a tree (the logits are FMA results, so
-            // fmaxf needs no canonicalising).
+            // 15 three-input maxima and one two-input in a tree (the logits are
+            // FMA results, so fmaxf needs no canonicalising).
             auto fmax3 = [](float a, float b, float c) __attribute__((always_inline)) {
                 return fmaxf(fmaxf(a, b), c);
             };
@@ -412,8 +412,8 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
                     if (32 * t + 8 * (r >> 2) + (r & 3) >= lim) sc[t][r] = NEG_INF_BITS;
         }
         // Row max over this lane's 32 keys (a v_max3 tree), then the partner half.
-        // 32 scores in 16 three-input maxima: 10 over 30 scores, 4 over those
-        // and the last two scores, then 2.
+        // 32 scores in 15 three-input maxima and one two-input: 10 over 30
+        // scores, 4 over those and the last two scores, then 1 + 1.
         auto max3 = [](int a, int b, int c) __attribute__((always_inline)) { return max(max(a, b), c); };
         int m3[10];
 #pragma unroll
