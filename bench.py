@@ -469,6 +469,9 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-peak", action="store_true", help="skip the MFMA peak probes")
+    ap.add_argument("--tile", default=None,
+                    help="WARPS,M_TILES,STAGES: the reference's Tile for the context (default Config::for_head_dim); "
+                         "warps 8 selects the eight-wave attention layout")
     ap.add_argument("--vggt", action="store_true",
                     help="instead of the headline line: the reference's gpu_bench workload (tests.rs:817-990), "
                          "VGGT-Omega global attention, 689-token frames (17 special + 21x32 patches), by default 16 heads of 64")
@@ -524,7 +527,10 @@ def main() -> int:
     q, k, v = synthetic(torch, args.config)
     out = torch.empty((B, N, H, D), dtype=q.dtype, device="cuda")
     stream = torch.cuda.current_stream()
-    sa = S.SageAttention(stream, D)
+    config = None
+    if args.tile:
+        config = S.Config(S.Tile(*(int(x) for x in args.tile.split(","))), S.PvAccum.F32)
+    sa = S.SageAttention(stream, D, config)
     shape = S.Shape(B, H, N, HK if HK != H else 0)
     ws = sa.workspace(shape)
     opts = S.Options(causal=causal)
@@ -594,7 +600,8 @@ def main() -> int:
         "dtype": "i8 QK^T (i32 acc) + e4m3 PV (f32 acc)",
         "data": "synthetic (torch.randn on the GPU; K offset per (head, channel) as the config states)",
         "config": {"workload": NAMES[args.config], "batch": B, "heads": H, "kv_heads": HK, "tokens": N,
-                   "head_dim": D, "causal": causal, "inputs": dt},
+                   "head_dim": D, "causal": causal, "inputs": dt,
+                   "tile": "{}w{}m{}s".format(*(lambda t: (t.warps, t.m_tiles, t.stages))(sa.config().tile))},
         "frac_of_peak": round(value / VENDOR_PEAK_TOPS, 4),
         "attention": {"ms": round(attn_ms, 4), "ms_min": round(attn_min, 4), "ms_mean": round(attn_mean, 4),
                       "reps": attn_reps, "settle_launches": settle,

@@ -60,10 +60,14 @@ typedef enum sage_pv_accum { SAGE_PV_F32 = 0, SAGE_PV_F16 = 1 } sage_pv_accum;
 
 /* Tile (mod.rs:116-168): the reference's CTA shape (warps, 16-row m-tiles per
  * warp, K/V ring stages; 16 * m_tiles * warps rows a CTA). Accepted exactly
- * as Tile::validate accepts it; it tunes the reference's NVIDIA kernel, and
- * every accepted tile runs here on the one CDNA4 configuration (4 wave64s of
- * 32 queries, 128 queries a workgroup, double-buffered K/V), so results do not
- * depend on it. */
+ * as Tile::validate accepts it. It picks the CDNA4 workgroup layout, never
+ * the results (every layout's outputs are bit-identical): warps = 8 (dense
+ * and causal attention, either head dim) runs eight wave64s a workgroup, four
+ * score waves (QK^T, softmax) and four output waves (rescale, P.V, one block
+ * behind) over the same 128 queries; every other tile, the defaults included,
+ * runs four wave64s of 32 queries, each doing the whole block. Both
+ * double-buffer K and V. KV-merged attention always runs the four-wave
+ * layout. */
 typedef struct sage_tile {
     uint32_t warps;
     uint32_t m_tiles;

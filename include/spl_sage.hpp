@@ -53,9 +53,10 @@ enum class Dtype : int32_t { Bf16 = SAGE_BF16, F16 = SAGE_F16 };
 enum class PvAccum : int32_t { F32 = SAGE_PV_F32, F16 = SAGE_PV_F16 };
 
 // Tile (mod.rs:116-168): the reference's CTA shape (warps, 16-row m-tiles,
-// K/V ring stages). Validated as the reference validates it; every valid
-// tile runs on the library's one CDNA4 configuration, so it does not change
-// results.
+// K/V ring stages). Validated as the reference validates it. It picks the
+// workgroup layout, never the results: warps = 8 (dense and causal
+// attention) runs eight waves a workgroup (score waves and output waves),
+// every other tile four waves that each do a whole block.
 struct Tile {
     uint32_t warps = 4, m_tiles = 2, stages = 3;
 

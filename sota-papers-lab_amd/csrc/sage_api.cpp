@@ -198,10 +198,10 @@ uint64_t sage_strides_extent(const sage_strides* s, uint64_t batch, uint64_t tok
 
 // Tile::validate (mod.rs:158-167): warps in {2, 4, 8}, m_tiles in {1, 2, 4},
 // stages 2..6, and the reference's rows per CTA (16 * m_tiles * warps)
-// dividing the 128-query tile. The tile tunes the reference's NVIDIA kernel;
-// every tile it accepts runs here on the one CDNA4 configuration (4 wave64s
-// of 32 queries, 128 queries a workgroup, double-buffered K/V), so outputs do
-// not depend on it.
+// dividing the 128-query tile. The tile picks the workgroup layout only
+// (attend_view): warps = 8 runs the eight-wave layout (score and output
+// waves) for dense and causal attention, every other tile the four-wave one;
+// outputs do not depend on it.
 sage_status sage_tile_validate(const sage_tile* t) {
     if (!t) return fail(SAGE_ERR_INVALID, "null tile");
     const bool warps_ok = t->warps == 2 || t->warps == 4 || t->warps == 8;
@@ -281,7 +281,7 @@ sage_status sage_attn_kernel_resources(const sage_attention* s, int32_t kernel, 
         return fail(SAGE_ERR_INVALID, "unknown attention kernel %d", kernel);
     int r = 0, sp = 0, l = 0;
     hipError_t e = sage::attention_resources((int)s->head_dim, kernel == SAGE_KERNEL_CAUSAL,
-                                             kernel == SAGE_KERNEL_MERGED, &r, &sp, &l);
+                                             kernel == SAGE_KERNEL_MERGED, s->config.tile.warps == 8, &r, &sp, &l);
     if (e != hipSuccess) return hip_fail(e, "registers");
     *regs = r;
     *spill = sp;
@@ -534,7 +534,8 @@ sage_status attend_view(const sage_attention* s, const WsView& w, const Geom& ge
     g.o_sb = (long long)out->strides.batch;
     g.o_st = (long long)out->strides.token;
     g.o_sh = (long long)out->strides.head;
-    g.flags = (g.flags & ~F_OUT_F16) | (out->dtype == SAGE_F16 ? F_OUT_F16 : 0);
+    g.flags = (g.flags & ~(F_OUT_F16 | F_WAVES8)) | (out->dtype == SAGE_F16 ? F_OUT_F16 : 0) |
+              (s->config.tile.warps == 8 ? F_WAVES8 : 0);
     AttendBufs bufs{w.q8, w.q_scale, w.k8, w.k_scale, w.v8, w.stats, w.kbias, out->data};
     hipError_t e = launch_attention((int)s->head_dim, bufs, g, s->stream);
     if (e != hipSuccess) return hip_fail(e, "launch sage attention");

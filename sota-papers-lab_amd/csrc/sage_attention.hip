@@ -557,6 +557,295 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
     }
 }
 
+#ifndef SAGE_ATTN_MERGED
+// Dense and causal, eight waves a workgroup: score waves and output waves
+// (the layout of Tile { warps: 8, .. }).
+//
+// An 8-wave workgroup owns 128 queries of one (batch, head). Waves 0-3, the
+// score waves, run QK^T and the online softmax of 32 queries each; waves 4-7,
+// the output waves, hold the O^T accumulators of the same queries (wave
+// w + 4 those of wave w) and run the rescale and P.V. The dispatcher places a
+// workgroup's waves round-robin over the CU's four SIMDs, so waves w and
+// w + 4 share a SIMD, and with two workgroups a CU (<= 128 VGPRs) every SIMD
+// runs two score waves and two output waves: a score wave's chain is QK^T
+// and softmax only, and the FP8 P.V MFMAs run under the softmax.
+//
+// Step j runs the softmax of block j on the score waves and the P.V of block
+// j - 1 on the output waves. A score wave hands each block's P^T operand (32
+// bytes a lane, the register layout of the MFMA's B operand) and its
+// per-query alpha to the output wave's same lane through LDS, double-buffered
+// like K and V; the V ring runs one block behind the K ring. One barrier a
+// step. The arithmetic is sage_attn<D, CAUSAL, false>'s, operation for
+// operation (the same logits, running max, P codes, row sums, rescale and
+// accumulation order), so the outputs are bit-identical to it. It runs two
+// query groups a SIMD where sage_attn runs three (head dim 128) or four (64),
+// and is the slower of the two on MI355X; the default tiles select sage_attn.
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(512, 2) void sage_attn_split(const int8_t* __restrict__ q8,
+                                                          const float* __restrict__ q_scale,
+                                                          const int8_t* __restrict__ k8,
+                                                          const float* __restrict__ k_scale,
+                                                          const uint8_t* __restrict__ v8,
+                                                          const float* __restrict__ stats,
+                                                          uint16_t* __restrict__ out, Geom g) {
+    constexpr int BN = ATTN_BN, KS = D / 32, DT = D / 32, TILE = BN * D, KCPR = D / 16;
+    // 16-byte chunks a K or V tile: 512 at head dim 128 (one a thread), 256 at
+    // 64 (one a thread of four waves: score waves copy K, output waves V).
+    constexpr int CHUNKS = TILE / 16;
+    static_assert(CHUNKS == 512 || CHUNKS == 256, "head dim 64 or 128");
+
+    __shared__ __attribute__((aligned(16))) uint8_t ldsK0[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsK1[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsV0[TILE];
+    __shared__ __attribute__((aligned(16))) uint8_t ldsV1[TILE];
+    // P^T operands of one block, [group][register half][lane] 16 bytes (a
+    // lane's two b128 accesses are 1 KB apart, conflict-free), and alpha
+    // [group][lane], double-buffered; the final row sums [group][lane].
+    __shared__ __attribute__((aligned(16))) uint4 ldsP0[4 * 2 * 64];
+    __shared__ __attribute__((aligned(16))) uint4 ldsP1[4 * 2 * 64];
+    __shared__ __attribute__((aligned(16))) float ldsA0[4 * 64];
+    __shared__ __attribute__((aligned(16))) float ldsA1[4 * 64];
+    __shared__ __attribute__((aligned(16))) float ldsL[4 * 64];
+
+    const int tid = threadIdx.x, lane = tid & 63, col = lane & 31, half = lane >> 5;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), grp = wv & 3;
+    const int ntq = gridDim.x;
+    const int lin = blockIdx.x + ntq * (blockIdx.y + gridDim.y * blockIdx.z), total = ntq * gridDim.y * gridDim.z;
+    int qt, hb;  // query tile; head slot b * heads + h (the same dealing as sage_attn)
+    if (CAUSAL && causal_longest_first(total, ntq)) {
+        const int per = total / NUM_XCD, hx = per / ntq, x = lin % NUM_XCD, i = lin / NUM_XCD;
+        qt = ntq - 1 - i / hx;
+        hb = x * hx + i % hx;
+    } else {
+        const int tile = xcd_tile(lin, total);
+        qt = CAUSAL ? ntq - 1 - tile % ntq : tile % ntq;
+        hb = tile / ntq;
+    }
+    const int h = hb % g.heads, b = hb / g.heads, hk = h / g.group;
+    const long long bh = (long long)b * g.heads + h, bhk = (long long)b * g.kv_heads + hk;
+    const int q0 = qt * ATTN_ROWS + grp * 32;  // first query of this wave's group
+
+    int nblk = g.kblocks;
+    if (CAUSAL) nblk = min(nblk, (qt * ATTN_ROWS + ATTN_ROWS - 1) / BN + 1);
+    int nfull = min(nblk, g.tk / BN);
+    if (CAUSAL) nfull = min(nfull, (qt * ATTN_ROWS + 1) / BN);
+
+    const uint8_t* kg = reinterpret_cast<const uint8_t*>(k8) + bhk * (long long)g.tk_pad * D;
+    const uint8_t* vg = v8 + bhk * (long long)g.tk_pad * D;
+
+    // Direct global -> LDS copies of 16-byte chunks: wave slot `sl` fills
+    // chunks 64 sl .. 64 sl + 63 of a tile (they land contiguously at M0;
+    // lane `lane` fetches the logical chunk the swizzle puts there).
+    const int sl = CHUNKS == 512 ? wv : (wv & 3);
+    const uint32_t fk = 16u * (uint32_t)swz(sl * 64 + lane, KCPR), fv = 16u * (uint32_t)swz(sl * 64 + lane, 4);
+    auto fetch = [&](const uint8_t* src_base, int blk, uint8_t* dst, uint32_t off) __attribute__((always_inline)) {
+        const uint8_t* tb = opaque_uniform(src_base + (long long)blk * TILE);
+        opaque_vgpr(off);
+        __builtin_amdgcn_global_load_lds(tb + (size_t)off,
+                                         (__attribute__((address_space(3))) void*)(dst + 16 * 64 * sl), 16, 0, 0);
+    };
+    const bool copies_k = CHUNKS == 512 || wv < 4, copies_v = CHUNKS == 512 || wv >= 4;
+    // Step j's copies: K(j + 1) for the next step's QK^T, V(j) for the next
+    // step's P.V.
+    auto prefetch = [&](int j, uint8_t* k_fill, uint8_t* v_fill) __attribute__((always_inline)) {
+        if (copies_k && j + 1 < nblk) fetch(kg, j + 1, k_fill, fk);
+        if (copies_v && j < nblk) fetch(vg, j, v_fill, fv);
+    };
+
+    if (copies_k) fetch(kg, 0, ldsK0, fk);
+    __syncthreads();
+
+    if (wv < 4) {
+        // ---- score wave: QK^T, online softmax, P^T and alpha to LDS ----
+        const int qi = q0 + col;
+        v4i qa[KS];
+        {
+            const int8_t* qrow = q8 + (bh * g.tq_pad + qi) * D + 16 * half;
+#pragma unroll
+            for (int s = 0; s < KS; s++) qa[s] = *reinterpret_cast<const v4i*>(qrow + 32 * s);
+        }
+        const float qs = fmaxf(q_scale[bh * (g.tq_pad / QGROUP) + (qi >> 4)], SCALE_FLOOR);
+#pragma unroll
+        for (int s = 0; s < KS; s++) asm volatile("" ::"v"(qa[s]));
+        asm volatile("" ::"v"(qs));
+        const float* ksc = k_scale + bhk * g.kblocks;
+        int koff[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ks++) koff[ks] = 16 * swz(col * KCPR + 2 * ks + half, KCPR);
+        v16i magic;
+#pragma unroll
+        for (int r = 0; r < 16; r++) magic[r] = MAGIC_BITS;
+        opaque_vgpr(magic);
+        float m = -1.0e30f, l = 0.f;
+
+        auto block = [&](int blk, const uint8_t* kt, uint4* pdst, float* adst) __attribute__((always_inline)) {
+            // The reference's fp32 operation order for the logits: no FMA contraction.
+#pragma clang fp contract(off)
+            // S^T of the block, keys 32t .. 32t + 31 in sc[t], from 1.5 * 2^23:
+            // a sub-tile's four K operand reads in one LDS round trip, then its
+            // four MFMAs.
+            v16i sc[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                uint4 ka[KS];
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++)
+                    ka[ks] = *reinterpret_cast<const uint4*>(kt + 16 * 32 * t * KCPR + koff[ks]);
+#pragma unroll
+                for (int ks = 0; ks < KS; ks++) {
+                    const v4i av = {(int)ka[ks].x, (int)ka[ks].y, (int)ka[ks].z, (int)ka[ks].w};
+                    sc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, qa[ks], ks ? sc[t] : magic, 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);  // the four LDS reads
+                __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);  // then the four MFMAs
+            }
+            const float kscf = scale_floor(ksc[blk]);
+            const float scl = qs * kscf;
+            const float xoff = -MAGIC * scl;
+            if (blk >= nfull) {
+                // Padding keys, and keys after the query when causal (as sage_attn).
+                const int ln = lane_now(), hf = ln >> 5;
+                int lim = g.tk - blk * BN - 4 * hf;
+                if (CAUSAL) lim = min(lim, q0 + (ln & 31) - blk * BN - 4 * hf + 1);
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        if (32 * t + 8 * (r >> 2) + (r & 3) >= lim) sc[t][r] = NEG_INF_BITS;
+            }
+            auto max3 = [](int a, int b, int c) __attribute__((always_inline)) { return max(max(a, b), c); };
+            int m3[10];
+#pragma unroll
+            for (int i = 0; i < 10; i++)
+                m3[i] = max3(sc[(3 * i) >> 4][(3 * i) & 15], sc[(3 * i + 1) >> 4][(3 * i + 1) & 15],
+                             sc[(3 * i + 2) >> 4][(3 * i + 2) & 15]);
+            const int m9 = max3(m3[0], m3[1], m3[2]), m10 = max3(m3[3], m3[4], m3[5]);
+            const int m11 = max3(m3[6], m3[7], m3[8]), m12 = max3(m3[9], sc[1][14], sc[1][15]);
+            int mx = max(max3(m9, m10, m11), m12);
+            mx = max_halves(mx);
+            const float mnew = running_max(m, fmaf(__int_as_float(mx), scl, xoff));
+            const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+            m = mnew;
+            const float off = (LOG2_448 - mnew) + xoff;
+            float p[2][16];
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) p[t][r] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sc[t][r]), scl, off));
+            float q16[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) q16[r] = p[0][r] + p[1][r];
+#pragma unroll
+            for (int w = 8; w > 0; w >>= 1)
+#pragma unroll
+                for (int r = 0; r < w; r++) q16[r] += q16[r + w];
+            l = fmaf(l, alpha, q16[0]);
+            v8i pn;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int t = j >> 2, r0 = 4 * (j & 3);
+                const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0], p[t][r0 + 1], 0, false);
+                pn[j] = __builtin_amdgcn_cvt_pk_fp8_f32(p[t][r0 + 2], p[t][r0 + 3], lo, true);
+            }
+            pdst[lane] = make_uint4((uint32_t)pn[0], (uint32_t)pn[1], (uint32_t)pn[2], (uint32_t)pn[3]);
+            pdst[64 + lane] = make_uint4((uint32_t)pn[4], (uint32_t)pn[5], (uint32_t)pn[6], (uint32_t)pn[7]);
+            adst[lane] = alpha;
+            if (blk == nblk - 1) ldsL[grp * 64 + lane] = l;
+        };
+        for (int j = 0; j <= nblk; j += 2) {
+            prefetch(j, ldsK1, ldsV0);
+            if (j < nblk) block(j, ldsK0, ldsP0 + grp * 128, ldsA0 + grp * 64);
+            __syncthreads();
+            if (j + 1 <= nblk) {
+                prefetch(j + 1, ldsK0, ldsV1);
+                if (j + 1 < nblk) block(j + 1, ldsK1, ldsP1 + grp * 128, ldsA1 + grp * 64);
+                __syncthreads();
+            }
+        }
+    } else {
+        // ---- output wave: rescale O by alpha, O^T += V^T P^T, epilogue ----
+        v16f o[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[dt][r] = 0.f;
+        const int voff0 = 16 * swz(col * 4 + 2 * half, 4), voff1 = 16 * swz(col * 4 + 2 * half + 1, 4);
+        auto block = [&](const uint8_t* vt, const uint4* psrc, const float* asrc) __attribute__((always_inline)) {
+            const float alpha = asrc[lane];
+            const uint4 p0 = psrc[lane], p1 = psrc[64 + lane];
+            uint4 va[DT][2];
+#pragma unroll
+            for (int d = 0; d < DT; d++) {
+                va[d][0] = *reinterpret_cast<const uint4*>(vt + 16 * 128 * d + voff0);
+                va[d][1] = *reinterpret_cast<const uint4*>(vt + 16 * 128 * d + voff1);
+            }
+            // alpha is exactly 1 in every row whose max did not move (the exp2
+            // of 0) and below 1 otherwise; multiplying by 1 changes nothing, so
+            // this is sage_attn's rescale.
+            if (__any(alpha < 1.0f)) {
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) o[dt][r] *= alpha;
+            }
+            const v8i pb = {(int)p0.x, (int)p0.y, (int)p0.z, (int)p0.w, (int)p1.x, (int)p1.y, (int)p1.z, (int)p1.w};
+#pragma unroll
+            for (int d = 0; d < DT; d++) {
+                const v8i av = {(int)va[d][0].x, (int)va[d][0].y, (int)va[d][0].z, (int)va[d][0].w,
+                                (int)va[d][1].x, (int)va[d][1].y, (int)va[d][1].z, (int)va[d][1].w};
+                o[d] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, pb, o[d], 0, 0, 0, 127, 0, 127);
+            }
+        };
+        for (int j = 0; j <= nblk; j += 2) {
+            prefetch(j, ldsK1, ldsV0);
+            if (j >= 1) block(ldsV1, ldsP1 + grp * 128, ldsA1 + grp * 64);  // block j - 1 (odd)
+            __syncthreads();
+            if (j + 1 <= nblk) {
+                prefetch(j + 1, ldsK0, ldsV1);
+                block(ldsV0, ldsP0 + grp * 128, ldsA0 + grp * 64);  // block j (even)
+                __syncthreads();
+            }
+        }
+
+        // out = O / l * v_scale + v_mean; lane holds channels 32dt + 8j + 4*half + 0..3.
+        const float lt = sum_halves(ldsL[grp * 64 + lane]);
+        const float inv = 1.0f / lt;
+        const int qi = q0 + col;
+        if (qi < g.tokens) {
+            const float* vmean = stats + bhk * 4 * D + D;
+            const float* vscale = vmean + D;
+            uint16_t* orow = out + b * g.o_sb + (long long)qi * g.o_st + h * g.o_sh;
+            auto emit = [&](auto pack) __attribute__((always_inline)) {
+#pragma unroll
+                for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int d0 = 32 * dt + 8 * j + 4 * half;
+                        float y[4];
+#pragma unroll
+                        for (int r = 0; r < 4; r++) y[r] = fmaf(o[dt][4 * j + r] * inv, vscale[d0 + r], vmean[d0 + r]);
+                        uint2 w;
+                        w.x = pack(y[0], y[1]);
+                        w.y = pack(y[2], y[3]);
+                        *reinterpret_cast<uint2*>(orow + d0) = w;
+                    }
+            };
+            if (g.flags & F_OUT_F16)
+                emit([](float a, float b) { return pack_f16x2(a, b); });
+            else
+                emit([](float a, float b) { return pack_bf16x2(a, b); });
+        }
+    }
+}
+
+template <int D, bool CAUSAL>
+static hipError_t launch_split(const AttendBufs& w, const Geom& g, hipStream_t s) {
+    hipLaunchKernelGGL((sage_attn_split<D, CAUSAL>), dim3(g.tq_pad / ATTN_ROWS, g.heads, g.batch), dim3(512), 0, s,
+                       w.q8, w.q_scale, w.k8, w.k_scale, w.v8, w.stats, static_cast<uint16_t*>(w.out), g);
+    return hipGetLastError();
+}
+#endif
+
 template <int D, bool CAUSAL, bool MERGE>
 static hipError_t launch_d(const AttendBufs& w, const Geom& g, hipStream_t s) {
     hipLaunchKernelGGL((sage_attn<D, CAUSAL, MERGE>), dim3(g.tq_pad / ATTN_ROWS, g.heads, g.batch), dim3(256), 0, s,
@@ -588,13 +877,32 @@ static hipError_t resources_of(int head_dim, int* regs, int* spill, int* lds) {
 // causal masking over merged keys.
 hipError_t launch_attention(int head_dim, const AttendBufs& w, const Geom& g, hipStream_t s) {
     if (g.merge > 1) return launch_attention_merged(head_dim, w, g, s);
+    if (g.flags & F_WAVES8) {
+        if (head_dim == 64)
+            return (g.flags & F_CAUSAL) ? launch_split<64, true>(w, g, s) : launch_split<64, false>(w, g, s);
+        return (g.flags & F_CAUSAL) ? launch_split<128, true>(w, g, s) : launch_split<128, false>(w, g, s);
+    }
     if (head_dim == 64)
         return (g.flags & F_CAUSAL) ? launch_d<64, true, false>(w, g, s) : launch_d<64, false, false>(w, g, s);
     return (g.flags & F_CAUSAL) ? launch_d<128, true, false>(w, g, s) : launch_d<128, false, false>(w, g, s);
 }
 
-hipError_t attention_resources(int head_dim, bool causal, bool merge, int* regs, int* spill, int* lds) {
+hipError_t attention_resources(int head_dim, bool causal, bool merge, bool waves8, int* regs, int* spill, int* lds) {
     if (merge) return attention_resources_merged(head_dim, regs, spill, lds);
+    if (waves8) {
+        hipFuncAttributes a;
+        const void* f = head_dim == 64
+                            ? (causal ? reinterpret_cast<const void*>(&sage_attn_split<64, true>)
+                                      : reinterpret_cast<const void*>(&sage_attn_split<64, false>))
+                            : (causal ? reinterpret_cast<const void*>(&sage_attn_split<128, true>)
+                                      : reinterpret_cast<const void*>(&sage_attn_split<128, false>));
+        hipError_t e = hipFuncGetAttributes(&a, f);
+        if (e != hipSuccess) return e;
+        *regs = a.numRegs;
+        *spill = (int)a.localSizeBytes;
+        *lds = (int)a.sharedSizeBytes;
+        return hipSuccess;
+    }
     return causal ? resources_of<true, false>(head_dim, regs, spill, lds)
                   : resources_of<false, false>(head_dim, regs, spill, lds);
 }

@@ -21,6 +21,7 @@ enum : int {
     F_CAUSAL = 16,   // extensions
     F_IN_F16 = 32,
     F_OUT_F16 = 64,
+    F_WAVES8 = 128,  // Tile { warps: 8 }: the eight-wave attention layout (dense and causal)
 };
 
 // Kernel parameter block, passed by value. Element strides of the 16-bit

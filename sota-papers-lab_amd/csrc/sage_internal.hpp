@@ -65,8 +65,9 @@ hipError_t launch_attention(int head_dim, const AttendBufs& w, const Geom& g, hi
 hipError_t launch_attention_merged(int head_dim, const AttendBufs& w, const Geom& g, hipStream_t s);
 
 // Kernel resources (VGPRs, scratch, LDS) of the attention kernel for
-// head_dim: dense, causal or KV-merged.
-hipError_t attention_resources(int head_dim, bool causal, bool merge, int* regs, int* spill, int* lds);
+// head_dim: dense, causal or KV-merged; waves8 = the eight-wave layout that
+// Tile { warps: 8 } selects for dense and causal attention.
+hipError_t attention_resources(int head_dim, bool causal, bool merge, bool waves8, int* regs, int* spill, int* lds);
 hipError_t attention_resources_merged(int head_dim, int* regs, int* spill, int* lds);
 
 // MFMA peak probe: which 0 = INT8, 1 = FP8, 2 = BF16; returns dense TOPS.

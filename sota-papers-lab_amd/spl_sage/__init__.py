@@ -48,9 +48,10 @@ def _check(status: int) -> None:
 @dataclass(frozen=True)
 class Tile:
     """mod.rs:116-168: the reference's CTA shape (warps, 16-row m-tiles,
-    K/V ring stages), validated as the reference validates it. Every valid
-    tile runs on the library's one CDNA4 configuration, so it does not change
-    results."""
+    K/V ring stages), validated as the reference validates it. It picks the
+    workgroup layout, never the results: warps = 8 (dense and causal
+    attention) runs eight waves a workgroup (score waves and output waves),
+    every other tile four waves that each do a whole block."""
 
     warps: int
     m_tiles: int
