@@ -95,16 +95,36 @@ __device__ __forceinline__ void layernorm8(float* x, const float* __restrict__ w
 // the codes equal those of running that prologue and then this one.
 template <int D>
 __device__ __forceinline__ void qkv_row(float* x, const QkvDev& qa, const QkvLane& L, const QkvTok& T, int part,
-                                        int ch) {
+                                        int ch, uint4* packed = nullptr) {
     qkv_apply<D>(x, qa, L, T, part, ch);
     // Pairs through one packed conversion: the low bf16 back to f32 by a
-    // shift, the high one by a mask.
+    // shift, the high one by a mask. `packed` receives the bf16 row itself.
+    uint32_t u[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
-        const uint32_t u = pack_bf16x2(x[e], x[e + 1]);
-        x[e] = __uint_as_float(u << 16);
-        x[e + 1] = __uint_as_float(u & 0xffff0000u);
+        u[e / 2] = pack_bf16x2(x[e], x[e + 1]);
+        x[e] = __uint_as_float(u[e / 2] << 16);
+        x[e + 1] = __uint_as_float(u[e / 2] & 0xffff0000u);
     }
+    if (packed) *packed = make_uint4(u[0], u[1], u[2], u[3]);
+}
+
+// The fused prologue's K stash. While sage_prep runs, the workspace's INT8 K
+// and FP8 V buffers hold nothing yet, and one 64-key block of them (64 D
+// bytes of k8, 64 D of v8) holds exactly that block's 64 K rows in bf16. So
+// sage_prep stores each K row as the QKV prologue leaves it (bf16) there --
+// keys 0-31 of block j over k8's block j, keys 32-63 over v8's -- and
+// sage_quant_kv reads them back instead of re-running the QKV arithmetic on
+// the projection; it reads a block's stash before it writes that block's
+// codes (its K-scale barrier lies between). Dense plans only: a merged
+// plan's blocks pool more tokens than the stash holds.
+__device__ __forceinline__ uint8_t* k_stash(int8_t* k8, uint8_t* v8, const Geom& g, long long bhk, int tok, int ch,
+                                            int D) {
+    const int blk = tok / KBLOCK, kk = tok % KBLOCK;
+    uint8_t* base = kk < KBLOCK / 2
+                        ? reinterpret_cast<uint8_t*>(k8) + (bhk * g.tk_pad + (long long)blk * KBLOCK) * D
+                        : v8 + (bhk * g.kblocks + blk) * (long long)(KBLOCK * D);
+    return base + (kk % (KBLOCK / 2)) * 2 * D + ch * 16;
 }
 
 // sage_quant.cu:59-160 (sg_prep), in two roles. Under QK LayerNorm (LN, the
@@ -116,8 +136,9 @@ __device__ __forceinline__ void qkv_row(float* x, const QkvDev& qa, const QkvLan
 // 97-107, 129-159): the tile's partial K sum, V sum, V min and V max.
 template <int D, bool LN, bool QKV>
 __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-                                           const float* __restrict__ ln, float* __restrict__ part, const Geom& g,
-                                           const QkvDev& qa, int tile, int hk, int b, float (*red)[4][D]) {
+                                           const float* __restrict__ ln, float* __restrict__ part, int8_t* k8,
+                                           uint8_t* v8, const Geom& g, const QkvDev& qa, int tile, int hk, int b,
+                                           float (*red)[4][D]) {
     constexpr int CH = D / 8;        // 16-byte chunks per head row
     constexpr int TPI = 256 / CH;    // tokens per iteration
     constexpr int NI = QTILE / TPI;  // iterations
@@ -163,8 +184,10 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
             qkv_tok<D>(tt, qa, g, 1, b, tok, ch);
             unpack8(load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, ok), fk, false);
             unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, ok), fv, false);
-            qkv_row<D>(fk, qa, lk, tt, 1, ch);
+            uint4 kbf;
+            qkv_row<D>(fk, qa, lk, tt, 1, ch, &kbf);
             qkv_row<D>(fv, qa, lv, tt, 2, ch);
+            if (g.merge == 1 && ok) *reinterpret_cast<uint4*>(k_stash(k8, v8, g, bhk, tok, ch, D)) = kbf;
             accumulate(tok, fk, fv);
         }
     } else {
@@ -293,7 +316,8 @@ template <int D, bool LN, bool QKV>
 __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                  const uint16_t* __restrict__ v, const float* __restrict__ ln,
                                                  int8_t* __restrict__ q8, float* __restrict__ q_scale,
-                                                 float* __restrict__ part, Geom g, QkvDev qa) {
+                                                 float* __restrict__ part, int8_t* __restrict__ k8,
+                                                 uint8_t* __restrict__ v8, Geom g, QkvDev qa) {
     __shared__ unsigned gmax[QTILE / QGROUP];
     __shared__ float red[8][4][D];
     const int roles = 1 + g.group, tile = (int)blockIdx.x / roles, role = (int)blockIdx.x % roles;
@@ -301,7 +325,7 @@ __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q,
     if (role)
         tile_q8<D, LN, QKV>(q, ln, q8, q_scale, g, qa, tile, hk, role - 1, b, gmax);
     else
-        tile_stats<D, LN, QKV>(k, v, ln, part, g, qa, tile, hk, b, red);
+        tile_stats<D, LN, QKV>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
 }
 
 // sage_quant.cu:163-206 (sg_finalize): even and odd tiles folded separately.
@@ -437,13 +461,15 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
                 put_v(vt, ch, kl, vq);
             }
         }
-        QkvLane lk;
-        qkv_lane<D>(lk, qa, g, 1, hk, ch);
+        // K rows as sage_prep stashed them (bf16, after the QKV arithmetic),
+        // over this block's k8 and v8 bytes: every read here is consumed
+        // before the K-scale barrier, every code store comes after it.
         uint4 kraw[NI];
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int j = blk * KBLOCK + slot + i * TPI;
-            kraw[i] = load16(k + b * g.k_sb + (long long)j * g.k_st + hk * g.k_sh + ch * 8, j < g.tk);
+            kraw[i] = j < g.tk ? *reinterpret_cast<const uint4*>(k_stash(k8, v8, g, bhk, j, ch, D))
+                               : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < NI; i++) {
@@ -451,9 +477,6 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
             const bool ok = blk * KBLOCK + kl < g.tk;
             float fk[8];
             unpack8(kraw[i], fk, false);
-            QkvTok tt;
-            qkv_tok<D>(tt, qa, g, 1, b, blk * KBLOCK + kl, ch);
-            qkv_row<D>(fk, qa, lk, tt, 1, ch);
             if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
@@ -702,7 +725,7 @@ static hipError_t launch_prologue_d(const uint16_t* q, const uint16_t* k, const 
                                     const PrologueBufs& w, const Geom& g, const QkvDev& qa, hipStream_t s) {
     hipLaunchKernelGGL((sage_prep<D, LN, QKV>), dim3((1 + g.group) * g.q_tiles, g.kv_heads, g.batch), dim3(256), 0, s,
                        q, k, v, ln,
-                       w.q8, w.q_scale, w.part, g, qa);
+                       w.q8, w.q_scale, w.part, w.k8, w.v8, g, qa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(sage_finalize<D>, dim3(g.kv_heads, g.batch), dim3(4 * D), 0, s, w.part, w.stats, g);

@@ -107,12 +107,18 @@ def test_standalone_prologue_is_bit_exact(oracle, torch_gpu, case):
             assert np.array_equal(g, w), (name, v_f16, int((g != w).sum()))
 
 
-FUSED = [  # (D, heads, kv, batch, tokens, norm, rope, scaled, causal, merge)
-    (64, 16, 0, 1, 2 * FRAME, 1, 0, True, False, 1),
-    (64, 16, 0, 1, 2 * FRAME, 2, 1, False, False, 4),
-    (128, 8, 2, 2, 1000, 1, 0, True, True, 1),
-    (128, 4, 0, 1, 777, 2, 1, False, False, 1),
-    (128, 4, 4, 1, 300, 0, None, True, False, 1),
+FUSED = [  # (D, heads, kv, batch, tokens, norm, rope, scaled, causal, merge, sage_ln)
+    (64, 16, 0, 1, 2 * FRAME, 1, 0, True, False, 1, False),
+    (64, 16, 0, 1, 2 * FRAME, 2, 1, False, False, 4, False),
+    (128, 8, 2, 2, 1000, 1, 0, True, True, 1, False),
+    (128, 4, 0, 1, 777, 2, 1, False, False, 1, False),
+    (128, 4, 4, 1, 300, 0, None, True, False, 1, False),
+    # the sage options' QkNorm on top of the QKV prologue's output (the LN and
+    # QKV instantiations together), dense and merged at both head dims
+    (64, 8, 0, 1, 2 * FRAME, 1, 0, True, False, 1, True),
+    (64, 8, 0, 1, 2 * FRAME, 2, 1, False, False, 4, True),
+    (128, 8, 2, 2, 1000, 1, 0, True, True, 1, True),
+    (128, 4, 0, 1, 2 * FRAME, 0, 0, True, False, 2, True),
 ]
 
 
@@ -122,14 +128,19 @@ def test_fused_prepare_equals_the_two_steps(oracle, torch_gpu, case):
     from spl_sage import qkv as Q
 
     torch = torch_gpu
-    D, H, kv, B, T, norm, rope, scaled, causal, merge = FUSED[case]
+    D, H, kv, B, T, norm, rope, scaled, causal, merge, sage_ln = FUSED[case]
     HK = kv or H
     rng = np.random.default_rng(200 + case)
     s, y = _spec(oracle, rng, D, H, kv, B, T, norm, rope, scaled)
     print(f"case {case}: D{D} H{H}/{HK} B{B} T{T} norm {norm} rope {rope} scaled {scaled} causal {causal} "
-          f"merge {merge}", flush=True)
+          f"merge {merge} sage QkNorm {sage_ln}", flush=True)
     layout = (T // FRAME, SPECIAL, GRID_H, GRID_W, 0) if merge > 1 else (1, 0, 0, 0, 0)
-    p = oracle.Problem(B, H, T, D, kv_heads=kv, dtype=0, causal=causal, merge=merge, layout=layout)
+    ln = None
+    if sage_ln:
+        ln = np.concatenate([1 + 0.2 * rng.standard_normal(D), 0.1 * rng.standard_normal(D),
+                             1 + 0.2 * rng.standard_normal(D), 0.1 * rng.standard_normal(D)]).astype(np.float32)
+    p = oracle.Problem(B, H, T, D, kv_heads=kv, dtype=0, causal=causal, merge=merge, layout=layout, ln=ln,
+                       ln_eps=1e-6)
     q16, k16, v16 = oracle.qkv_prologue(s, y)
     want = oracle.prologue(p, q16, k16, v16)
 
@@ -138,7 +149,8 @@ def test_fused_prepare_equals_the_two_steps(oracle, torch_gpu, case):
     km = S.KvMerge.Pool(merge, S.FrameLayout(*layout)) if merge > 1 else S.KvMerge.Dense
     ws = sa.workspace(S.Shape(B, H, T, kv), km)
     out = torch.empty((B, T, H, D), dtype=torch.bfloat16, device="cuda")
-    sa.forward_qkv(ws, inp, S.TensorMut(out), qn, rp, S.Options(causal=causal))
+    qk_norm = S.QkNorm(torch.from_numpy(ln.copy()).to("cuda"), 1e-6) if sage_ln else None
+    sa.forward_qkv(ws, inp, S.TensorMut(out), qn, rp, S.Options(causal=causal, qk_norm=qk_norm))
     torch.cuda.synchronize()
     assert_prologue_equal(read_workspace(ws, p), want)
     o_fused = from_device16(out)
