@@ -327,7 +327,11 @@ sage_status sage_rope_table(int32_t layout, uint64_t head_dim, uint64_t grid_h, 
  * ("qkv: ld .. must be a multiple of 8 and at least ..", "qkv: LayerNorm
  * QK-norm needs q and k biases", "qkv: RoPE frame length is 0", "<what>:
  * buffer holds .. elements, needs ..", "device pointer .. is not 16-byte
- * aligned"). An empty shape is a no-op, as there. */
+ * aligned") in the reference's order: ld, then the sizes of y, the scales
+ * and the bias, of q, k and v, of the norm weights and the RoPE table, and
+ * last the alignment of y, chan, bias, q, k and v (16 bytes). The norm
+ * weights and the RoPE table, f32, need only their type's alignment, as
+ * there. An empty shape is a no-op, as there. */
 sage_status sage_qkv_prologue(const sage_attention* s, const sage_shape* shape, const sage_qkv_in* in,
                               const sage_qkv_norm* norm, const sage_qkv_rope* rope, const sage_tensor_mut* q,
                               const sage_tensor_mut* k, const sage_tensor_mut* v);

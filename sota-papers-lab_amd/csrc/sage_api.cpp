@@ -254,6 +254,10 @@ sage_status sage_new(void* stream, uint64_t head_dim, const sage_config* config,
     if (e != hipSuccess) return hip_fail(e, "current device");
     st = sage_check_device(dev);
     if (st != SAGE_OK) return st;
+    // sage_forward_noalloc's scratch address on this device, looked up now so
+    // that the entry point itself only launches kernels.
+    st = sage::noalloc_init(dev);
+    if (st != SAGE_OK) return st;
     // No C++ exception may cross the C ABI: allocation failure is a status.
     sage_attention* s = new (std::nothrow) sage_attention;
     if (!s) return fail(SAGE_ERR_DEVICE, "out of host memory");
@@ -605,11 +609,15 @@ bool aligned(const void* p, uintptr_t bytes, sage_status* st) {
     return true;
 }
 
-// QkvPrologue::run's checks (qkv.rs:226-278) for batch x tokens tokens of
-// heads / kv_heads heads of dimension d, in the reference's order, and the
-// kernels' options. *bs receives the batch stride of y.
-sage_status qkv_setup(uint64_t batch, uint64_t tokens, uint64_t heads, uint64_t kv, uint64_t d, const sage_qkv_in* in,
-                      const sage_qkv_norm* norm, const sage_qkv_rope* rope, sage::QkvDev* qa, uint64_t* bs) {
+// QkvPrologue::run's checks (qkv.rs:226-279) for batch x tokens tokens of
+// heads / kv_heads heads of dimension d, in three parts taken in the
+// reference's order: the input buffers' sizes (qkv_inputs), then the
+// outputs' (the caller's), then the norm and RoPE options (qkv_options), and
+// last the alignment of y, chan, bias and the outputs (qkv_aligned; the
+// norm weights and the RoPE table, f32, need no more than their type's).
+// *bs receives the batch stride of y.
+sage_status qkv_inputs(uint64_t batch, uint64_t tokens, uint64_t heads, uint64_t kv, uint64_t d,
+                       const sage_qkv_in* in, sage::QkvDev* qa, uint64_t* bs) {
     sage_status st = SAGE_OK;
     const uint64_t width = (heads + 2 * kv) * d;
     const uint64_t stride = in->batch_stride ? in->batch_stride : tokens * in->ld;
@@ -627,6 +635,12 @@ sage_status qkv_setup(uint64_t batch, uint64_t tokens, uint64_t heads, uint64_t 
     qa->tok = in->tok;
     qa->chan = in->chan;
     qa->bias = in->bias;
+    *bs = stride;
+    return SAGE_OK;
+}
+
+sage_status qkv_options(uint64_t d, const sage_qkv_norm* norm, const sage_qkv_rope* rope, sage::QkvDev* qa) {
+    sage_status st = SAGE_OK;
     if (norm) {
         if (norm->kind != SAGE_QKV_LAYER_NORM && norm->kind != SAGE_QKV_RMS_NORM)
             return fail(SAGE_ERR_INVALID, "qkv: unknown QK-norm kind %d", norm->kind);
@@ -639,9 +653,6 @@ sage_status qkv_setup(uint64_t batch, uint64_t tokens, uint64_t heads, uint64_t 
                 return fail(SAGE_ERR_INVALID, "qkv: LayerNorm QK-norm needs q and k biases");
             if (!holds(norm->len, d, "q norm bias", &st) || !holds(norm->len, d, "k norm bias", &st)) return st;
         }
-        const void* ps[4] = {norm->q_weight, norm->q_bias, norm->k_weight, norm->k_bias};
-        for (const void* p : ps)
-            if (p && !aligned(p, 16, &st)) return st;
         qa->norm = norm->kind;
         qa->nw[0] = norm->q_weight;
         qa->nw[1] = norm->q_bias;
@@ -659,7 +670,6 @@ sage_status qkv_setup(uint64_t batch, uint64_t tokens, uint64_t heads, uint64_t 
             return rope->table ? st
                                : fail(SAGE_ERR_INVALID, "RoPE table: buffer holds 0 elements, needs %llu",
                                       (u64)(rope->frame_len * d));
-        if (!aligned(rope->table, 16, &st)) return st;
         qa->rope = rope->table;
         qa->rope_half = (int)(rope->layout == SAGE_ROPE_VGGT ? d / 4 : d / 2);
         qa->rope_shift = 0;
@@ -673,10 +683,19 @@ sage_status qkv_setup(uint64_t batch, uint64_t tokens, uint64_t heads, uint64_t 
         qa->fl_shift = l;
         qa->fl_magic = (uint32_t)(((1ull << 32) * ((1ull << l) - fl)) / fl + 1);
     }
+    return SAGE_OK;
+}
+
+// check_aligned (qkv.rs:279) over y, chan, bias and the outputs (outs, n of
+// them; 16-byte vector loads and stores), plus the per-token scales' f32.
+sage_status qkv_aligned(const sage_qkv_in* in, const void* const* outs, int n) {
+    sage_status st = SAGE_OK;
     if (!aligned(in->y, 16, &st) || (in->chan && !aligned(in->chan, 16, &st)) ||
-        (in->bias && !aligned(in->bias, 16, &st)) || (in->tok && !aligned(in->tok, 4, &st)))
+        (in->bias && !aligned(in->bias, 16, &st)))
         return st;
-    *bs = stride;
+    for (int i = 0; i < n; i++)
+        if (!aligned(outs[i], 16, &st)) return st;
+    if (in->tok && !aligned(in->tok, 4, &st)) return st;
     return SAGE_OK;
 }
 
@@ -739,7 +758,7 @@ sage_status sage_qkv_prologue(const sage_attention* s, const sage_shape* shape, 
                     (u64)shape->batch, (u64)(heads + 2 * kv));
     sage::QkvDev qa;
     uint64_t bs = 0;
-    st = qkv_setup(shape->batch, shape->tokens, heads, kv, d, in, norm, rope, &qa, &bs);
+    st = qkv_inputs(shape->batch, shape->tokens, heads, kv, d, in, &qa, &bs);
     if (st != SAGE_OK) return st;
     const sage_tensor_mut* outs[3] = {q, k, v};
     const char* names[3] = {"qkv q", "qkv k", "qkv v"};
@@ -749,7 +768,7 @@ sage_status sage_qkv_prologue(const sage_attention* s, const sage_shape* shape, 
         st = sage_strides_check(&t->strides, names[i]);
         if (st != SAGE_OK) return st;
         const uint64_t need = sage_strides_extent(&t->strides, shape->batch, shape->tokens, i ? kv : heads, d);
-        if (!holds(t->len, need, names[i], &st) || !aligned(t->data, 16, &st)) return st;
+        if (!holds(t->len, need, names[i], &st)) return st;
         const bool f16_ok = i == 2;
         if (t->dtype != SAGE_BF16 && !(f16_ok && t->dtype == SAGE_F16))
             return fail(SAGE_ERR_INVALID, "%s must be bf16%s", names[i], f16_ok ? " or fp16" : "");
@@ -759,6 +778,11 @@ sage_status sage_qkv_prologue(const sage_attention* s, const sage_shape* shape, 
         o.sh[i] = (long long)t->strides.head;
     }
     o.v_f16 = v->dtype == SAGE_F16;
+    st = qkv_options(d, norm, rope, &qa);
+    if (st != SAGE_OK) return st;
+    const void* out_ptrs[3] = {q->data, k->data, v->data};
+    st = qkv_aligned(in, out_ptrs, 3);
+    if (st != SAGE_OK) return st;
     sage::Geom g{};
     g.batch = (int)shape->batch;
     g.heads = (int)heads;
@@ -783,7 +807,9 @@ sage_status sage_prepare_qkv(const sage_attention* s, sage_workspace* ws, const 
     if (!qkv_ld_ok(in, (heads + 2 * kv) * d, &st)) return st;
     sage::QkvDev qa;
     uint64_t bs = 0;
-    st = qkv_setup(sh.batch, sh.tokens, heads, kv, d, in, norm, rope, &qa, &bs);
+    st = qkv_inputs(sh.batch, sh.tokens, heads, kv, d, in, &qa, &bs);
+    if (st == SAGE_OK) st = qkv_options(d, norm, rope, &qa);
+    if (st == SAGE_OK) st = qkv_aligned(in, nullptr, 0);
     if (st != SAGE_OK) return st;
     // Q, K and V as views into the projection: q | k | v along the channels.
     const uint16_t* y = static_cast<const uint16_t*>(in->y);

@@ -77,16 +77,16 @@ __device__ __forceinline__ float sum_halves(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
     return __int_as_float((int)r[0]) + __int_as_float((int)r[1]);
 }
-// Floor of the Q and K scales in the attention kernel: 1e-18, whose square is
-// still a normal float.
-constexpr float SCALE_FLOOR = 1.0e-18f;
-constexpr unsigned SCALE_FLOOR_BITS = 0x219392EFu;  // bits of 1e-18f
-// max(k_scale, 1e-18) of a wave-uniform k_scale (>= 0: amax / 127) as an
-// integer max of the bits (non-negative floats order like their bit
-// patterns): one scalar instruction a block instead of a VALU one.
-__device__ __forceinline__ float scale_floor(float s) {
-    return __uint_as_float(max(__float_as_uint(s), SCALE_FLOOR_BITS));
-}
+// Floor of the logit scale q_scale * k_scale in masked blocks: a masked score
+// is -inf and must stay -inf through the product (0 * -inf would be a NaN),
+// so the product is floored where scores are masked. Below 1e-30
+// the floor changes no result: every logit difference of the block is then
+// under 2^22 * 1e-30 < 1e-23, far below half an ulp of the exp2 argument
+// (about 8.8, ulp 2^-20), so every P and alpha come out bit-identical to the
+// unfloored product's. Only an exact zero scale (an all-zero 16-row Q group,
+// a K head constant over tokens) is changed: the row attends uniformly to its
+// visible keys, where the reference's masked keys turn into NaNs.
+constexpr float SCALE_FLOOR = 1.0e-30f;
 // max(m, x) for the running max: v_med3_f32(m, x, FLT_MAX) in one instruction
 // (fmaxf on the loop-carried m costs a canonicalising v_max_f32 m, m every
 // block). Neither operand is a NaN: m starts at -1e30 and x is a finite logit
@@ -200,11 +200,8 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
 #pragma unroll
         for (int s = 0; s < KS; s++) qa[s] = *reinterpret_cast<const v4i*>(qrow + 32 * s);
     }
-    // The Q scale floored at 1e-18; the K scale gets the same floor in the key
-    // loop (scale_floor), so q_scale * k_scale is a normal float above zero
-    // and a masked -inf score times it stays -inf. Only all-but-zero scales
-    // (amax below about 1e-16) are raised.
-    const float qs = fmaxf(q_scale[bh * (g.tq_pad / QGROUP) + (qi >> 4)], SCALE_FLOOR);
+    // The Q scale; the key loop floors its product with the K scale (SCALE_FLOOR).
+    const float qs = q_scale[bh * (g.tq_pad / QGROUP) + (qi >> 4)];
     // The Q scales of the wave's two 16-query groups (wave-uniform).
     const float qsg0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qs), 0));
     const float qsg1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(qs), QGROUP));
@@ -328,10 +325,12 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
                        __attribute__((always_inline)) {
         // The reference's fp32 operation order for the logits: no FMA contraction.
 #pragma clang fp contract(off)
-        // q_scale * k_scale, both floored (above), so that -inf * scl stays -inf.
-        const float kscf = scale_floor(ksc[blk]);
-        const float scl = qs * kscf;
-        const float xoff = -MAGIC * scl;
+        // The logit scale q_scale * k_scale, the reference's. A masked block
+        // sets scores to -inf, which the product must keep (0 * -inf is a NaN),
+        // so there it is floored at SCALE_FLOOR, which changes no result but an
+        // exact zero scale's; merged keys are masked by a -inf bias instead.
+        const float kscf = ksc[blk];
+        float scl = qs * kscf;
         if constexpr (MERGE) {
             // The logit fmaf(1.5 * 2^23 + S, scl, fmaf(-1.5 * 2^23, scl, bias)):
             // the inner term depends only on the key and the query group, so
@@ -410,7 +409,9 @@ __global__ __launch_bounds__(256, D == 64 ? 4 : (MERGE ? 2 : 3)) void sage_attn(
 #pragma unroll
                 for (int r = 0; r < 16; r++)
                     if (32 * t + 8 * (r >> 2) + (r & 3) >= lim) sc[t][r] = NEG_INF_BITS;
+            scl = fmaxf(scl, SCALE_FLOOR);
         }
+        const float xoff = -MAGIC * scl;
         // Row max over this lane's 32 keys (a v_max3 tree), then the partner half.
         // 32 scores in 15 three-input maxima and one two-input: 10 over 30
         // scores, 4 over those and the last two scores, then 1 + 1.
@@ -664,7 +665,7 @@ __global__ __launch_bounds__(512, 2) void sage_attn_split(const int8_t* __restri
 #pragma unroll
             for (int s = 0; s < KS; s++) qa[s] = *reinterpret_cast<const v4i*>(qrow + 32 * s);
         }
-        const float qs = fmaxf(q_scale[bh * (g.tq_pad / QGROUP) + (qi >> 4)], SCALE_FLOOR);
+        const float qs = q_scale[bh * (g.tq_pad / QGROUP) + (qi >> 4)];
 #pragma unroll
         for (int s = 0; s < KS; s++) asm volatile("" ::"v"(qa[s]));
         asm volatile("" ::"v"(qs));
@@ -699,9 +700,8 @@ __global__ __launch_bounds__(512, 2) void sage_attn_split(const int8_t* __restri
                 __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);  // the four LDS reads
                 __builtin_amdgcn_sched_group_barrier(0x008, KS, 0);  // then the four MFMAs
             }
-            const float kscf = scale_floor(ksc[blk]);
-            const float scl = qs * kscf;
-            const float xoff = -MAGIC * scl;
+            // The logit scale, floored in masked blocks only (as sage_attn).
+            float scl = qs * ksc[blk];
             if (blk >= nfull) {
                 // Padding keys, and keys after the query when causal (as sage_attn).
                 const int ln = lane_now(), hf = ln >> 5;
@@ -712,7 +712,9 @@ __global__ __launch_bounds__(512, 2) void sage_attn_split(const int8_t* __restri
 #pragma unroll
                     for (int r = 0; r < 16; r++)
                         if (32 * t + 8 * (r >> 2) + (r & 3) >= lim) sc[t][r] = NEG_INF_BITS;
+                scl = fmaxf(scl, SCALE_FLOOR);
             }
+            const float xoff = -MAGIC * scl;
             auto max3 = [](int a, int b, int c) __attribute__((always_inline)) { return max(max(a, b), c); };
             int m3[10];
 #pragma unroll

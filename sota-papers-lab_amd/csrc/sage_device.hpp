@@ -224,8 +224,13 @@ __device__ __forceinline__ int qkv_slot(const Geom& g, int part, int h) {
 template <int D>
 __device__ __forceinline__ void qkv_lane(QkvLane& L, const QkvDev& a, const Geom& g, int part, int h, int ch) {
     const int c0 = qkv_slot(g, part, h) * D + ch * 8;
+    // f32 arrays need only 4-byte alignment (the reference checks none for
+    // the norm weights, qkv.rs:279): 16-byte loads through memcpy assume no
+    // more, and gfx950 serves them as one global_load_dwordx4 either way.
     auto load8 = [](const float* p, float* o) {
-        const float4 u = *reinterpret_cast<const float4*>(p), v = *reinterpret_cast<const float4*>(p + 4);
+        float4 u, v;
+        __builtin_memcpy(&u, p, 16);
+        __builtin_memcpy(&v, p + 4, 16);
         o[0] = u.x, o[1] = u.y, o[2] = u.z, o[3] = u.w, o[4] = v.x, o[5] = v.y, o[6] = v.z, o[7] = v.w;
     };
     if (a.chan) load8(a.chan + c0, L.chan);
@@ -245,9 +250,10 @@ __device__ __forceinline__ void qkv_tok(QkvTok& T, const QkvDev& a, const Geom& 
         // Pair of the lane's first channel: (d0 / (2 half)) half + d0 % half.
         const int d0 = ch * 8, sh = a.rope_shift;
         const int pair0 = ((d0 >> (sh + 1)) << sh) + (d0 & (a.rope_half - 1));
-        const float4* row = reinterpret_cast<const float4*>(a.rope + (long long)rope_row(a, tok) * D + 2 * pair0);
+        // 4-byte alignment suffices, as for the norm weights (qkv_lane).
+        const float* row = a.rope + (long long)rope_row(a, tok) * D + 2 * pair0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) T.cs[i] = row[i];
+        for (int i = 0; i < 4; i++) __builtin_memcpy(&T.cs[i], row + 4 * i, 16);
     }
 }
 

@@ -92,6 +92,10 @@ struct WsView {
     float* part;
 };
 
+// Resolves the no-allocation entry point's scratch array on `device`, the
+// current device (once per device; sage_new calls it).
+sage_status noalloc_init(int device);
+
 // Sets this thread's sage_last_error() text; returns st.
 sage_status set_error(sage_status st, const char* fmt, ...);
 

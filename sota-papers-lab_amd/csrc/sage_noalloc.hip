@@ -6,8 +6,9 @@
 // The array `scratch` (SAGE_NOALLOC_MAX_BYTES) exists once on every GPU the
 // library is loaded on, from the code object's load until the process ends.
 // Its device address is looked up with hipGetSymbolAddress once per device,
-// with that device current, and only that address is handed to kernels: in
-// host code `scratch` names a host-side stand-in, not device memory.
+// with that device current, when a context is created there (sage_new), and
+// only that address is handed to kernels: in host code `scratch` names a
+// host-side stand-in, not device memory.
 //
 // Every call on one GPU shares that GPU's array and leaves its contents
 // behind. The prologue writes every element the attention kernel reads
@@ -28,33 +29,43 @@ static __device__ __align__(256) uint8_t scratch[SAGE_NOALLOC_MAX_BYTES];
 std::mutex g_mu;
 std::vector<void*> g_scratch;  // device address of `scratch`, per device ordinal
 
-// The device address of `scratch` on `device`, looked up once per device with
-// that device current (the caller's current device is restored).
+// The device address of `scratch` on `device`, as sage_new resolved it. The
+// entry point itself makes no HIP runtime call besides its kernel launches,
+// so a caller can capture even its first call on a device in a graph.
 sage_status scratch_address(int device, void** out) {
     std::lock_guard<std::mutex> lock(g_mu);
-    if (device < 0) return sage::set_error(SAGE_ERR_DEVICE, "no HIP device %d", device);
-    if ((size_t)device < g_scratch.size() && g_scratch[device]) {
+    if (device >= 0 && (size_t)device < g_scratch.size() && g_scratch[device]) {
         *out = g_scratch[device];
         return SAGE_OK;
     }
-    int cur = 0;
-    hipError_t e = hipGetDevice(&cur);
-    if (e == hipSuccess && cur != device) e = hipSetDevice(device);
-    void* p = nullptr;
-    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (cur != device) (void)hipSetDevice(cur);
-    if (e != hipSuccess || !p)
-        return sage::set_error(SAGE_ERR_DEVICE, "no-allocation scratch address on device %d: %s (%s)", device,
-                               hipGetErrorName(e), hipGetErrorString(e));
-    if ((size_t)device >= g_scratch.size()) g_scratch.resize((size_t)device + 1, nullptr);
-    g_scratch[device] = p;
-    *out = p;
-    return SAGE_OK;
+    return sage::set_error(SAGE_ERR_STATE, "no-allocation scratch of device %d was not resolved (sage_new does it)",
+                           device);
 }
 
 uint64_t round256(uint64_t x) { return (x + 255) & ~uint64_t(255); }
 
 }  // namespace
+
+namespace sage {
+
+// Looks up `scratch`'s device address on `device`, which must be the current
+// device (sage_new calls it with the context's device current), once per
+// device; later calls find it cached.
+sage_status noalloc_init(int device) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (device < 0) return set_error(SAGE_ERR_DEVICE, "no HIP device %d", device);
+    if ((size_t)device < g_scratch.size() && g_scratch[device]) return SAGE_OK;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+        return set_error(SAGE_ERR_DEVICE, "no-allocation scratch address on device %d: %s (%s)", device,
+                         hipGetErrorName(e), hipGetErrorString(e));
+    if ((size_t)device >= g_scratch.size()) g_scratch.resize((size_t)device + 1, nullptr);
+    g_scratch[device] = p;
+    return SAGE_OK;
+}
+
+}  // namespace sage
 
 extern "C" sage_status sage_forward_noalloc(const sage_attention* s, const sage_shape* shape,
                                             const sage_kv_merge* merge, const sage_tensor* q, const sage_tensor* k,

@@ -105,6 +105,27 @@ def test_zero_scales(oracle, torch_gpu, d):
     _check_attention(oracle, p, want, o, np.arange(p.tokens, dtype=np.int32), q, k, v, f"zero scales d{d}")
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_tiny_q_scale_against_huge_k_scale(oracle, torch_gpu, d):
+    """q_scale near 1e-23 against k_scale near 1e11 (bf16 Q ~ 1e-20, K ~ 1e13):
+    their product, about 1e-12, is the reference's logit scale and must be used
+    as is, with no floor on either factor (a floor of 1e-18 on q_scale would
+    scale every logit up by about 1e5 and sharpen the rows far past the gate).
+    Causal over a ragged tail, so masked -inf scores meet the product too."""
+    p = oracle.Problem(1, 2, 333, d, causal=True)
+    rng = np.random.default_rng(42)
+    qf = (rng.standard_normal((1, p.tokens, 2, d)) * 1e-20).astype(np.float32)
+    kf = (rng.standard_normal((1, p.tokens, 2, d)) * 1e13).astype(np.float32)
+    vf = rng.standard_normal((1, p.tokens, 2, d)).astype(np.float32)
+    q, k, v = (oracle.encode16(x, p.dtype) for x in (qf, kf, vf))
+    pro, o = run(torch_gpu, p, q, k, v)
+    want = oracle.prologue(p, q, k, v)
+    assert_prologue_equal(pro, want)
+    sc = want["q_scale"].max() * want["k_scale"].max()
+    assert 1e-14 < sc < 1e-10, sc  # the regime a per-factor floor would change
+    _check_attention(oracle, p, want, o, np.arange(p.tokens, dtype=np.int32), q, k, v, f"tiny q, huge k d{d}")
+
+
 @pytest.mark.parametrize("layout", ["packed", "bhtd"])
 def test_strided_layouts(oracle, torch_gpu, layout):
     p, g = oracle.Problem(2, 3, 389, 64), oracle.GenSpec(k_off_std=2.0, seed=13)

@@ -233,3 +233,58 @@ def test_refusals_carry_the_references_text(oracle, torch_gpu):
     with pytest.raises(S.SageError, match=r"qkv: ld 396 must be a multiple of 8"):
         sa.prepare_qkv(ws, bad, qn, rp)
     pro.run(Q.QkvIn(inp.y, s.ld), 0, 2, None, None, outs)  # empty: a no-op, as the reference
+
+
+def test_check_order_and_alignment_follow_the_reference(oracle, torch_gpu):
+    """qkv.rs:249-279: output sizes are checked before the norm and RoPE
+    options, and alignment last, over y, chan, bias, q, k and v only: norm
+    weights and a RoPE table at a 4-byte (not 16-byte) offset are accepted
+    and give the same bits as aligned copies."""
+    import spl_sage as S
+    from spl_sage import qkv as Q
+
+    torch = torch_gpu
+    rng = np.random.default_rng(8)
+    T, H, D = 300, 2, 64
+    s, y = _spec(oracle, rng, D, H, 0, 1, T, 1, 0, True)
+    inp, qn, rp = _device(torch, s, y)
+    sa = S.SageAttention(None, D)
+    pro = Q.QkvPrologue(sa)
+
+    def outs(n=T, offset=0):
+        ts = [torch.empty(1 * n * H * D + 8, dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+        return ts, Q.QkvOut(*(S.TensorMut(t[offset:offset + n * H * D].view(1, n, H, D)) for t in ts))
+
+    # 4-byte offsets of every norm weight and of the RoPE table
+    def shifted(t):
+        b = torch.empty(t.numel() + 1, dtype=torch.float32, device="cuda")
+        b[1:].copy_(t.reshape(-1))
+        return b[1:]
+    qn4 = Q.QkNorm(qn.kind, shifted(qn.q_weight), shifted(qn.k_weight), shifted(qn.q_bias), shifted(qn.k_bias),
+                   qn.eps)
+    rp4 = Q.Rope(shifted(rp.table), rp.layout, rp.frame_len)
+    assert qn4.q_weight.data_ptr() % 16 == 4 and rp4.table.data_ptr() % 16 == 4
+    (a, o_a), (b, o_b) = outs(), outs()
+    pro.run(inp, T, H, qn, rp, o_a)
+    pro.run(inp, T, H, qn4, rp4, o_b)
+    torch.cuda.synchronize()
+    n = T * H * D  # the written elements (each buffer has 8 more)
+    for x, z in zip(a, b):
+        assert torch.equal(x[:n].view(torch.int16), z[:n].view(torch.int16))
+    ws_a, ws_b = sa.workspace(S.Shape(1, H, T)), sa.workspace(S.Shape(1, H, T))
+    sa.prepare_qkv(ws_a, inp, qn, rp)
+    sa.prepare_qkv(ws_b, inp, qn4, rp4)
+    torch.cuda.synchronize()
+    for name in ("q8", "k8", "v8", "q_scale", "k_scale", "stats"):
+        assert torch.equal(ws_a.tensor(name), ws_b.tensor(name)), name
+
+    # a short output is reported before a LayerNorm without biases
+    _, short = outs(T - 1)
+    with pytest.raises(S.SageError, match="qkv q: buffer holds"):
+        pro.run(inp, T, H, Q.QkNorm(Q.NormKind.LayerNorm, qn.q_weight, qn.k_weight), rp, short)
+    # a misaligned output is reported after the RoPE checks, before any launch
+    _, skew = outs(offset=2)
+    with pytest.raises(S.SageError, match="qkv: RoPE frame length is 0"):
+        pro.run(inp, T, H, qn, Q.Rope(rp.table, rp.layout, 0), skew)
+    with pytest.raises(S.SageError, match="is not 16-byte aligned"):
+        pro.run(inp, T, H, qn, rp, skew)

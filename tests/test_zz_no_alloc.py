@@ -75,3 +75,64 @@ def test_noalloc_refuses_shapes_beyond_its_scratch(torch_gpu):
         sa.forward_noalloc(S.Shape(1, 32, n), S.Tensor(x), S.Tensor(x), S.Tensor(x), S.TensorMut(out))
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
+
+
+_CAPTURE_CHILD = r'''
+import sys
+import numpy as np
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import torch
+import spl_sage as S
+
+torch.cuda.set_device(0)
+B, H, N, D = 2, 4, 700, 128
+shape = S.Shape(B, H, N)
+rng = np.random.default_rng(5)
+def rnd():
+    return torch.from_numpy(rng.standard_normal((B, N, H, D)).astype(np.float32)).cuda().to(torch.bfloat16)
+q, k, v = rnd(), rnd(), rnd()
+stream = torch.cuda.Stream()
+sa = S.SageAttention(stream, D)  # resolves the no-allocation scratch on this device
+out_g = torch.empty_like(q)
+out_e = torch.empty_like(q)
+ws = sa.workspace(shape)
+with torch.cuda.stream(stream):  # the kernels' first launches, outside any capture
+    sa.forward(ws, S.Tensor(q), S.Tensor(k), S.Tensor(v), S.TensorMut(out_e))
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=stream):  # this process's first sage_forward_noalloc call
+    sa.forward_noalloc(shape, S.Tensor(q), S.Tensor(k), S.Tensor(v), S.TensorMut(out_g))
+torch.cuda.synchronize()
+for rep in range(4):
+    q.copy_(rnd()); k.copy_(rnd()); v.copy_(rnd())
+    torch.cuda.synchronize()
+    out_g.fill_(0)
+    graph.replay()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        sa.forward(ws, S.Tensor(q), S.Tensor(k), S.Tensor(v), S.TensorMut(out_e))
+    torch.cuda.synchronize()
+    a = out_g.view(torch.int16).cpu().numpy()
+    b = out_e.view(torch.int16).cpu().numpy()
+    if not np.array_equal(a, b):
+        print(f"replay {rep}: {int((a != b).sum())} outputs differ from sage_forward", flush=True)
+        sys.exit(1)
+print("CAPTURE_OK", flush=True)
+'''
+
+
+def test_first_noalloc_call_under_graph_capture(torch_gpu, tmp_path):
+    """A fresh process's first sage_forward_noalloc call, captured in a HIP
+    graph: the scratch address was resolved by sage_new, so the call only
+    launches kernels; every replay (new inputs between them) equals
+    sage_forward bit for bit."""
+    import subprocess
+    import sys
+
+    from conftest import PKG, ROOT
+
+    script = tmp_path / "capture_noalloc.py"
+    script.write_text(_CAPTURE_CHILD)
+    r = subprocess.run([sys.executable, "-u", str(script), str(ROOT), str(PKG)], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and "CAPTURE_OK" in r.stdout, (r.returncode, r.stdout[-2000:], r.stderr[-2000:])
