@@ -117,7 +117,6 @@ __device__ __forceinline__ void opaque_vgpr(T& x) {
 // tiles [x * per, (x + 1) * per): the workgroups that share a head's K and V
 // then read them through one L2 instead of eight. The last total % 8 tiles
 // keep their place.
-constexpr int NUM_XCD = 8;
 __device__ __forceinline__ int xcd_tile(int lin, int total) {
     const int per = total / NUM_XCD;
     if (lin >= per * NUM_XCD) return lin;

@@ -12,6 +12,7 @@ namespace sage {
 constexpr int QGROUP = 16;  // query rows per INT8 Q scale
 constexpr int QTILE = 128;  // queries per prologue tile (one K/V statistics partial)
 constexpr int KBLOCK = 64;  // keys per K scale and per V block
+constexpr int NUM_XCD = 8;  // MI355X's XCDs, each with its own L2; workgroups are dealt to them round-robin
 
 enum : int {
     F_LN_Q = 1,      // flag values of the reference's SgGeom::flags (sage_common.cu:26-29)

@@ -133,8 +133,14 @@ __device__ __forceinline__ uint8_t* k_stash(int8_t* k8, uint8_t* v8, const Geom&
 // the LN-free instantiation keeps the dense kernel's registers.
 
 // K and V channel statistics of one 128-token tile (sage_quant.cu:73-80,
-// 97-107, 129-159): the tile's partial K sum, V sum, V min and V max.
-template <int D, bool LN, bool QKV>
+// 97-107, 129-159): the tile's partial K sum, V sum, V min and V max. PART
+// selects the rows a workgroup reads: S_KV both (the reference's one block),
+// S_K the K rows and their sum, S_V the V rows and their sum, min and max. The
+// fused QKV prologue gives K and V workgroups of their own: K rows carry the
+// whole QKV arithmetic (norm, RoPE) and V rows little, so one workgroup doing
+// both was the slowest role of the launch.
+enum { S_KV = 0, S_K = 1, S_V = 2 };
+template <int D, bool LN, bool QKV, int PART>
 __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                            const float* __restrict__ ln, float* __restrict__ part, int8_t* k8,
                                            uint8_t* v8, const Geom& g, const QkvDev& qa, int tile, int hk, int b,
@@ -142,6 +148,7 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
     constexpr int CH = D / 8;        // 16-byte chunks per head row
     constexpr int TPI = 256 / CH;    // tokens per iteration
     constexpr int NI = QTILE / TPI;  // iterations
+    constexpr bool DO_K = PART != S_V, DO_V = PART != S_K;
     const int tid = threadIdx.x, ch = tid % CH, slot = tid / CH;
     const bool f16 = g.flags & F_IN_F16;
     const long long bhk = (long long)b * g.kv_heads + hk;
@@ -155,23 +162,44 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
     }
     QkvLane lk, lv;
     if (QKV) {
-        qkv_lane<D>(lk, qa, g, 1, hk, ch);
-        qkv_lane<D>(lv, qa, g, 2, hk, ch);
+        if (DO_K) qkv_lane<D>(lk, qa, g, 1, hk, ch);
+        if (DO_V) qkv_lane<D>(lv, qa, g, 2, hk, ch);
     }
     // Row i of the thread (token tok) into the running sums, in i order.
     auto accumulate = [&](int tok, float* fk, float* fv) __attribute__((always_inline)) {
-        if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
+        if (LN && DO_K) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
         if (tok < g.tokens) {
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                ks[e] += fk[e];
-                vs[e] += fv[e];
-                vmn[e] = fminf(vmn[e], fv[e]);
-                vmx[e] = fmaxf(vmx[e], fv[e]);
+                if (DO_K) ks[e] += fk[e];
+                if (DO_V) {
+                    vs[e] += fv[e];
+                    vmn[e] = fminf(vmn[e], fv[e]);
+                    vmx[e] = fmaxf(vmx[e], fv[e]);
+                }
             }
         }
     };
-    if constexpr (QKV) {
+    if constexpr (QKV && PART == S_V) {
+        // V rows carry only the token and channel scales and the bias: all
+        // loads first, as for plain inputs.
+        uint4 vraw[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int tok = tile * QTILE + slot + i * TPI;
+            vraw[i] = load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, tok < g.tokens);
+        }
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int tok = tile * QTILE + slot + i * TPI;
+            float fv[8];
+            QkvTok tt;
+            qkv_tok<D>(tt, qa, g, 2, b, tok, ch);
+            unpack8(vraw[i], fv, false);
+            qkv_row<D>(fv, qa, lv, tt, 2, ch);
+            accumulate(tok, nullptr, fv);
+        }
+    } else if constexpr (QKV) {
         // Rows of the fused projection carry their QKV-prologue arithmetic;
         // two at a time keeps the registers of more waves (other waves hide
         // the loads' latency).
@@ -183,10 +211,10 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
             QkvTok tt;
             qkv_tok<D>(tt, qa, g, 1, b, tok, ch);
             unpack8(load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, ok), fk, false);
-            unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, ok), fv, false);
+            if (DO_V) unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, ok), fv, false);
             uint4 kbf;
             qkv_row<D>(fk, qa, lk, tt, 1, ch, &kbf);
-            qkv_row<D>(fv, qa, lv, tt, 2, ch);
+            if (DO_V) qkv_row<D>(fv, qa, lv, tt, 2, ch);
             if (g.merge == 1 && ok) *reinterpret_cast<uint4*>(k_stash(k8, v8, g, bhk, tok, ch, D)) = kbf;
             accumulate(tok, fk, fv);
         }
@@ -214,10 +242,12 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
     for (int o = CH; o < 32; o <<= 1) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            ks[e] += __shfl_xor(ks[e], o, 64);
-            vs[e] += __shfl_xor(vs[e], o, 64);
-            vmn[e] = fminf(vmn[e], __shfl_xor(vmn[e], o, 64));
-            vmx[e] = fmaxf(vmx[e], __shfl_xor(vmx[e], o, 64));
+            if (DO_K) ks[e] += __shfl_xor(ks[e], o, 64);
+            if (DO_V) {
+                vs[e] += __shfl_xor(vs[e], o, 64);
+                vmn[e] = fminf(vmn[e], __shfl_xor(vmn[e], o, 64));
+                vmx[e] = fmaxf(vmx[e], __shfl_xor(vmx[e], o, 64));
+            }
         }
     }
     if ((tid & 31) < CH) {
@@ -230,7 +260,8 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
         }
     }
     __syncthreads();
-    for (int c = tid; c < 4 * D; c += 256) {
+    constexpr int S0 = DO_K ? 0 : 1, S1 = DO_V ? 4 : 1;  // the statistics [S0, S1) this part owns
+    for (int c = S0 * D + tid; c < S1 * D; c += 256) {
         const int stat = c / D, d = c % D;
         float r = red[0][stat][d];
 #pragma unroll
@@ -307,11 +338,14 @@ __device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const fl
     }
 }
 
-// 1 + group workgroups a tile: the first the K/V statistics, each other the
+// STATS + group workgroups a tile: the first STATS the K/V statistics (one,
+// or with the fused QKV prologue one for K and one for V), each other the
 // INT8 Q of one query head of the KV head's group. The reference's one
 // thread block does all of it in turn; split, the streams of loads overlap
 // across workgroups, and grouped-query plans spread their Q heads over
 // workgroups instead of walking them in one.
+template <bool QKV>
+constexpr int stat_roles() { return QKV ? 2 : 1; }
 template <int D, bool LN, bool QKV>
 __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                  const uint16_t* __restrict__ v, const float* __restrict__ ln,
@@ -320,61 +354,108 @@ __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q,
                                                  uint8_t* __restrict__ v8, Geom g, QkvDev qa) {
     __shared__ unsigned gmax[QTILE / QGROUP];
     __shared__ float red[8][4][D];
-    const int roles = 1 + g.group, tile = (int)blockIdx.x / roles, role = (int)blockIdx.x % roles;
+    constexpr int STATS = stat_roles<QKV>();
+    const int roles = STATS + g.group, tile = (int)blockIdx.x / roles, role = (int)blockIdx.x % roles;
     const int hk = blockIdx.y, b = blockIdx.z;
-    if (role)
-        tile_q8<D, LN, QKV>(q, ln, q8, q_scale, g, qa, tile, hk, role - 1, b, gmax);
+    if (role >= STATS)
+        tile_q8<D, LN, QKV>(q, ln, q8, q_scale, g, qa, tile, hk, role - STATS, b, gmax);
+    else if (!QKV)
+        tile_stats<D, LN, QKV, S_KV>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
+    else if (role == 0)
+        tile_stats<D, LN, QKV, S_K>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
     else
-        tile_stats<D, LN, QKV>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
+        tile_stats<D, LN, QKV, S_V>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
 }
 
-// sage_quant.cu:163-206 (sg_finalize): even and odd tiles folded separately.
-// One thread per (statistic, channel); the tile partials are loaded sixteen
-// at a time (eight even/odd pairs in flight) and folded in tile order.
+// sage_quant.cu:163-206 (sg_finalize): even and odd tiles folded separately,
+// each in tile order, then combined. A workgroup takes FIN_CH channels of one
+// KV head, i.e. their 4 * FIN_CH (statistic, channel) columns. Its 256
+// threads stage up to FIN_CHUNK tiles of those columns in LDS with every load
+// of the chunk in flight at once; wave w then folds statistic w, one lane per
+// (channel, parity), in tile order, so the fold's operation is uniform across
+// the wave. A long sequence (VGGT's 1077 tiles a head) costs a few load
+// round trips instead of one per sixteen tiles. The workgroups of one head
+// share every 128-byte line of its partials, so they are dealt to one XCD
+// (the dispatcher deals linear ids round-robin over the 8 XCDs): each line
+// then comes from HBM into one L2 once.
+constexpr int FIN_CH = 4;
+constexpr int FIN_CHUNK = 512;
 template <int D>
-__global__ __launch_bounds__(4 * D) void sage_finalize(const float* __restrict__ part, float* __restrict__ stats,
-                                                       Geom g) {
-    constexpr int BATCH = 8;  // even/odd pairs loaded before folding
-    const int hk = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-    const long long bhk = (long long)b * g.kv_heads + hk;
-    __shared__ float st[4][D];
-    {
-        const int stat = tid / D, d = tid % D;
-        const float* p = part + bhk * g.q_tiles * 4 * D + stat * D + d;
-        float r0 = stat < 2 ? 0.f : (stat == 2 ? 3.0e38f : -3.0e38f);
-        float r1 = r0;
-        auto fold = [&](float& r, float x) {
-            r = stat < 2 ? r + x : (stat == 2 ? fminf(r, x) : fmaxf(r, x));
-        };
-        const int pairs = g.q_tiles / 2;
-        int t2 = 0;
-        for (; t2 + BATCH <= pairs; t2 += BATCH) {
-            float x0[BATCH], x1[BATCH];
+__global__ __launch_bounds__(256) void sage_finalize(const float* __restrict__ part, float* __restrict__ stats,
+                                                     Geom g) {
+    constexpr int NCG = D / FIN_CH;
+    __shared__ float4 tl[FIN_CHUNK][4];  // [tile][statistic]: the workgroup's FIN_CH channels
+    __shared__ float fin[4][2][FIN_CH];
+    const int lin = (int)blockIdx.x, j = lin / NUM_XCD, tid = threadIdx.x;
+    const int cg = j % NCG;
+    const long long bhk = (long long)(j / NCG) * NUM_XCD + lin % NUM_XCD;
+    if (bhk >= (long long)g.batch * g.kv_heads) return;  // the grid pads heads to a multiple of 8
+    const float* base = part + bhk * g.q_tiles * 4 * D + cg * FIN_CH;
+    // Folding lanes: statistic = wave (uniform), channel fc, tile parity par.
+    const int fs = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int fc = lane & (FIN_CH - 1), par = (lane >> 2) & 1;
+    const bool folds = lane < 2 * FIN_CH;
+    float r = fs < 2 ? 0.f : (fs == 2 ? 3.0e38f : -3.0e38f);
+    // Loading threads: tile tid / 4 + 64 i of the chunk, statistic tid % 4.
+    const int ls = tid & 3, lt = tid >> 2;
+    // A chunk's loads are all in flight together, and the next chunk's while
+    // this one is folded. Only the 64-tile slices a chunk reaches are loaded
+    // (a workgroup-uniform count); rows past the sequence inside them are
+    // filled from its last tile and never folded.
+    const float* src = base + (long long)lt * 4 * D + ls * D;
+    const long long last = (long long)(g.q_tiles - 1 - lt) * 4 * D;  // clamp, relative to src
+    auto slices = [&](int t0) { return max(0, min(FIN_CHUNK / 64, (g.q_tiles - t0 + 63) / 64)); };
+    // (Held as scalars: an array of float4 copied into LDS whole was kept in
+    // scratch memory by the compiler.)
+    float x[FIN_CHUNK / 64][4];
+    auto fetch = [&](int i, long long off) __attribute__((always_inline)) {
+        const float4 u = *reinterpret_cast<const float4*>(src + min(off, last));
+        x[i][0] = u.x, x[i][1] = u.y, x[i][2] = u.z, x[i][3] = u.w;
+    };
+    int nl = slices(0);
 #pragma unroll
-            for (int i = 0; i < BATCH; i++) {
-                x0[i] = p[(long long)(2 * (t2 + i)) * 4 * D];
-                x1[i] = p[(long long)(2 * (t2 + i) + 1) * 4 * D];
-            }
+    for (int i = 0; i < FIN_CHUNK / 64; i++)
+        if (i < nl) fetch(i, (long long)(64 * i) * 4 * D);
+    for (int t0 = 0; t0 < g.q_tiles; t0 += FIN_CHUNK) {
+        const int n = min(FIN_CHUNK, g.q_tiles - t0);
 #pragma unroll
-            for (int i = 0; i < BATCH; i++) {
-                fold(r0, x0[i]);
-                fold(r1, x1[i]);
+        for (int i = 0; i < FIN_CHUNK / 64; i++)
+            if (i < nl) tl[lt + 64 * i][ls] = make_float4(x[i][0], x[i][1], x[i][2], x[i][3]);
+        __syncthreads();
+        nl = slices(t0 + FIN_CHUNK);
+#pragma unroll
+        for (int i = 0; i < FIN_CHUNK / 64; i++)
+            if (i < nl) fetch(i, (long long)(t0 + FIN_CHUNK + 64 * i) * 4 * D);
+        // t0 is even, so a tile's parity in the chunk is its parity overall.
+        if (folds) {
+            const float* col = reinterpret_cast<const float*>(&tl[0][fs]) + fc;
+            if (fs < 2) {
+#pragma unroll 8
+                for (int t = par; t < n; t += 2) r += col[t * 16];
+            } else if (fs == 2) {
+#pragma unroll 8
+                for (int t = par; t < n; t += 2) r = fminf(r, col[t * 16]);
+            } else {
+#pragma unroll 8
+                for (int t = par; t < n; t += 2) r = fmaxf(r, col[t * 16]);
             }
         }
-        for (; t2 < pairs; t2++) {
-            fold(r0, p[(long long)(2 * t2) * 4 * D]);
-            fold(r1, p[(long long)(2 * t2 + 1) * 4 * D]);
-        }
-        if (g.q_tiles & 1) fold(r0, p[(long long)(g.q_tiles - 1) * 4 * D]);
-        st[stat][d] = stat < 2 ? r0 + r1 : (stat == 2 ? fminf(r0, r1) : fmaxf(r0, r1));
+        __syncthreads();
     }
+    if (folds) fin[fs][par][fc] = r;
     __syncthreads();
-    if (tid < D) {
-        const int d = tid;
+    if (tid < FIN_CH) {
+        const int c = tid, d = cg * FIN_CH + c;
+        float st[4];
+#pragma unroll
+        for (int s2 = 0; s2 < 4; s2++) {
+            const float r0 = fin[s2][0][c], r1 = fin[s2][1][c];
+            st[s2] = s2 < 2 ? r0 + r1 : (s2 == 2 ? fminf(r0, r1) : fmaxf(r0, r1));
+        }
         const float n = (float)g.tokens;
-        const float mk = (g.flags & F_SMOOTH_K) ? st[0][d] / n : 0.f;
-        const float mv = (g.flags & F_SMOOTH_V) ? st[1][d] / n : 0.f;
-        const float amax = fmaxf(st[3][d] - mv, mv - st[2][d]);
+        const float mk = (g.flags & F_SMOOTH_K) ? st[0] / n : 0.f;
+        const float mv = (g.flags & F_SMOOTH_V) ? st[1] / n : 0.f;
+        const float amax = fmaxf(st[3] - mv, mv - st[2]);
         const float scale = amax > 0.f ? amax / g.v_range : 1.0f;
         float* o = stats + bhk * 4 * D;
         o[d] = mk;
@@ -723,12 +804,16 @@ hipError_t launch_qkv(int head_dim, const uint16_t* y, const QkvOutDev& o, const
 template <int D, bool LN, bool QKV>
 static hipError_t launch_prologue_d(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* ln,
                                     const PrologueBufs& w, const Geom& g, const QkvDev& qa, hipStream_t s) {
-    hipLaunchKernelGGL((sage_prep<D, LN, QKV>), dim3((1 + g.group) * g.q_tiles, g.kv_heads, g.batch), dim3(256), 0, s,
+    const long long prep_blocks = (long long)(stat_roles<QKV>() + g.group) * g.q_tiles;
+    if (prep_blocks > INT32_MAX) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL((sage_prep<D, LN, QKV>), dim3((unsigned)prep_blocks, g.kv_heads, g.batch), dim3(256), 0, s,
                        q, k, v, ln,
                        w.q8, w.q_scale, w.part, w.k8, w.v8, g, qa);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(sage_finalize<D>, dim3(g.kv_heads, g.batch), dim3(4 * D), 0, s, w.part, w.stats, g);
+    const long long heads8 = ((long long)g.batch * g.kv_heads + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
+    if (heads8 * (D / FIN_CH) > INT32_MAX) return hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(sage_finalize<D>, dim3((unsigned)(heads8 * (D / FIN_CH))), dim3(256), 0, s, w.part, w.stats, g);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((sage_quant_kv<D, LN, QKV>), dim3(g.kblocks, g.kv_heads, g.batch), dim3(256), 0, s, k, v, ln,

@@ -43,12 +43,17 @@ def _case(oracle, name):
         # tiles longest first across each XCD's head slots (2 and 1 slots per XCD).
         "d128_causal_b2_xcd": (P(2, 8, 700, 128, kv_heads=4, causal=True), G(k_off_std=2.0, seed=13)),
         "d64_causal_b2_xcd": (P(2, 4, 260, 64, dtype=1, causal=True), G(k_off_std=2.0, seed=14)),
+        # More 128-token tiles than the statistics fold stages at once (512):
+        # three chunks with an odd tile count, and two chunks at head dim 128.
+        "d64_t139900": (P(1, 2, 139900, 64), G(k_off_std=3.0, seed=15)),
+        "d128_t66000": (P(1, 1, 66000, 128, dtype=1), G(k_off_std=2.0, seed=16)),
     }
     return cases[name]
 
 
 SMALL = ["c1", "d128_tail200", "d64_t3001", "d128_gqa", "d64_nosmooth", "d128_causal_f16", "d64_causal_gqa",
-         "n1", "n65", "tokens_x10", "outlier_ch20", "d128_causal_b2_xcd", "d64_causal_b2_xcd"]
+         "n1", "n65", "tokens_x10", "outlier_ch20", "d128_causal_b2_xcd", "d64_causal_b2_xcd", "d64_t139900",
+         "d128_t66000"]
 
 
 def _check_attention(oracle, p, pro_oracle, o_gpu, rows, q, k, v, label, rows_f64=None):
@@ -88,8 +93,8 @@ def test_small_cases(oracle, torch_gpu, name):
 def test_zero_scales(oracle, torch_gpu, d):
     """Degenerate scales: a K head constant over tokens (K smoothing leaves
     zeros, so every k_scale of that head is 0) and an all-zero 16-row Q group
-    (q_scale 0), causal over a ragged tail. The attention kernel floors both
-    scales before their product multiplies a masked -inf score; the reference
+    (q_scale 0), causal over a ragged tail. The attention kernel floors the
+    product of the scales where it multiplies masked -inf scores; the reference
     arithmetic has no floor, and a zero scale makes every logit of the row 0,
     so both give uniform attention over the visible keys. Codes bit-exact;
     outputs finite and at the gate on every row."""
