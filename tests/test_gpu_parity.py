@@ -47,13 +47,16 @@ def _case(oracle, name):
         # three chunks with an odd tile count, and two chunks at head dim 128.
         "d64_t139900": (P(1, 2, 139900, 64), G(k_off_std=3.0, seed=15)),
         "d128_t66000": (P(1, 1, 66000, 128, dtype=1), G(k_off_std=2.0, seed=16)),
+        # Exactly one full chunk (512 tiles), and one more tile holding one token.
+        "d128_t65536": (P(1, 1, 65536, 128), G(k_off_std=2.0, seed=17)),
+        "d64_t65537": (P(1, 1, 65537, 64, dtype=1), G(k_off_std=2.0, seed=18)),
     }
     return cases[name]
 
 
 SMALL = ["c1", "d128_tail200", "d64_t3001", "d128_gqa", "d64_nosmooth", "d128_causal_f16", "d64_causal_gqa",
          "n1", "n65", "tokens_x10", "outlier_ch20", "d128_causal_b2_xcd", "d64_causal_b2_xcd", "d64_t139900",
-         "d128_t66000"]
+         "d128_t66000", "d128_t65536", "d64_t65537"]
 
 
 def _check_attention(oracle, p, pro_oracle, o_gpu, rows, q, k, v, label, rows_f64=None):
