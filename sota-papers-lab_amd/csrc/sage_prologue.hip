@@ -6,8 +6,11 @@
 //                  tile, one workgroup writes the partial K sum, V sum, V min,
 //                  V max of every channel, and one per query head of the
 //                  group that shares the KV head its INT8 Q (Q and K rows
-//                  LayerNormed first under QK LayerNorm)
-//   sage_finalize  grid (kv_heads, batch): K mean, V mean, V scale, 1/V scale
+//                  LayerNormed first under QK LayerNorm); fed from the fused
+//                  QKV projection, K and V get a workgroup each
+//                  ((2 + group) q_tiles)
+//   sage_finalize  grid (D / 4 channel groups of every KV head, dealt one
+//                  head an XCD): K mean, V mean, V scale, 1/V scale
 //   sage_quant_kv  grid (kblocks, kv_heads, batch): smoothed INT8 K and FP8 V,
 //                  V transposed per 64-key block into the MFMA operand order;
 //                  with KV merging each key pools its members (and the keys'
@@ -127,7 +130,7 @@ __device__ __forceinline__ uint8_t* k_stash(int8_t* k8, uint8_t* v8, const Geom&
     return base + (kk % (KBLOCK / 2)) * 2 * D + ch * 16;
 }
 
-// sage_quant.cu:59-160 (sg_prep), in two roles. Under QK LayerNorm (LN, the
+// sage_quant.cu:59-160 (sg_prep), split into roles (statistics, Q codes). Under QK LayerNorm (LN, the
 // F_LN_Q and F_LN_K flags together as the reference sets them) every K row is
 // normalised before the statistics read it and every Q row before its amax;
 // the LN-free instantiation keeps the dense kernel's registers.
