@@ -11,6 +11,8 @@ platform/spl-nn/src/qkv.rs, cuda/qkv.cu), through the C ABI:
   and the attention output equals the unfused GPU path (sage_qkv_prologue,
   then prepare and attend) bit for bit, and meets the north-star gate;
 - RoPE rows t % frame_len at frame lengths 1, 38, 64 and 4096, both paths;
+- seeded random fused problems (every option drawn together), bit for bit
+  against the oracle and the two GPU steps;
 - the reference's refusals, before any launch."""
 from __future__ import annotations
 
@@ -288,3 +290,71 @@ def test_check_order_and_alignment_follow_the_reference(oracle, torch_gpu):
         pro.run(inp, T, H, qn, Q.Rope(rp.table, rp.layout, 0), skew)
     with pytest.raises(S.SageError, match="is not 16-byte aligned"):
         pro.run(inp, T, H, qn, rp, skew)
+
+
+FUZZ_CASES = 16
+
+
+def _fuzz_case(rng):
+    """A random fused-prologue problem: head dim, heads and grouping, batch,
+    ragged token count (past one statistics-fold chunk now and then), norm
+    kind, RoPE layout or none, token and channel scales or none, causal or
+    KV-merged keys, and the sage QkNorm on top."""
+    D = int(rng.choice([64, 128]))
+    H = int(rng.integers(1, 7))
+    kv = int(rng.choice([x for x in range(1, H + 1) if H % x == 0]))
+    B = int(rng.integers(1, 3))
+    merge = int(rng.choice([1, 1, 1, 2, 4]))
+    if merge > 1:
+        grid = (int(rng.integers(2, 9)), int(rng.integers(2, 11)), int(rng.integers(0, 6)))
+        frames = int(rng.integers(1, 4))
+        T = frames * (grid[2] + grid[0] * grid[1])
+        layout = (frames, grid[2], grid[0], grid[1], int(rng.integers(0, frames + 1)))
+        causal = False
+    else:
+        grid = (int(rng.integers(1, 12)), int(rng.integers(1, 40)), int(rng.integers(0, 20)))
+        T = int(rng.integers(1, 900))
+        if rng.random() < 0.2:  # past one fold chunk (512 tiles), kept to a head or two
+            T, H, kv, B = int(rng.integers(65000, 67000)), min(H, 2), 1, 1
+        layout = (1, 0, 0, 0, 0)
+        causal = bool(rng.random() < 0.3)
+    norm = int(rng.integers(0, 3))
+    rope = None if rng.random() < 0.25 else int(rng.integers(0, 2))
+    return dict(D=D, H=H, kv=kv if kv != H else 0, B=B, T=T, norm=norm, rope=rope, scaled=bool(rng.random() < 0.6),
+                causal=causal, merge=merge, layout=layout, grid=grid, sage_ln=bool(rng.random() < 0.25))
+
+
+@pytest.mark.parametrize("case", range(FUZZ_CASES))
+def test_fused_prepare_fuzz(oracle, torch_gpu, case):
+    """Seeded random fused problems (the K, V and Q workgroups of the
+    statistics pass, the K stash of dense plans, the merged path): the
+    workspace equals the oracle prologue of the oracle QKV prologue's bf16 Q,
+    K and V bit for bit, and the output equals the two GPU steps' bit for bit."""
+    import spl_sage as S
+
+    torch = torch_gpu
+    rng = np.random.default_rng(5000 + case)
+    c = _fuzz_case(rng)
+    D, H, kv, B, T = c["D"], c["H"], c["kv"], c["B"], c["T"]
+    print(f"case {case}: {c}", flush=True)
+    s, y = _spec(oracle, rng, D, H, kv, B, T, c["norm"], c["rope"], c["scaled"], grid=c["grid"])
+    ln = None
+    if c["sage_ln"]:
+        ln = np.concatenate([1 + 0.2 * rng.standard_normal(D), 0.1 * rng.standard_normal(D),
+                             1 + 0.2 * rng.standard_normal(D), 0.1 * rng.standard_normal(D)]).astype(np.float32)
+    p = oracle.Problem(B, H, T, D, kv_heads=kv, dtype=0, causal=c["causal"], merge=c["merge"], layout=c["layout"],
+                       ln=ln, ln_eps=1e-6)
+    q16, k16, v16 = oracle.qkv_prologue(s, y)
+    want = oracle.prologue(p, q16, k16, v16)
+
+    inp, qn, rp = _device(torch, s, y)
+    sa = S.SageAttention(None, D)
+    km = S.KvMerge.Pool(c["merge"], S.FrameLayout(*c["layout"])) if c["merge"] > 1 else S.KvMerge.Dense
+    ws = sa.workspace(S.Shape(B, H, T, kv), km)
+    out = torch.empty((B, T, H, D), dtype=torch.bfloat16, device="cuda")
+    qk_norm = S.QkNorm(torch.from_numpy(ln.copy()).to("cuda"), 1e-6) if c["sage_ln"] else None
+    sa.forward_qkv(ws, inp, S.TensorMut(out), qn, rp, S.Options(causal=c["causal"], qk_norm=qk_norm))
+    torch.cuda.synchronize()
+    assert_prologue_equal(read_workspace(ws, p), want)
+    _, o_two = run(torch, p, q16, k16, v16, want_ws=False)
+    assert np.array_equal(from_device16(out), o_two)
