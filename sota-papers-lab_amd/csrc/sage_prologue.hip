@@ -281,12 +281,14 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
 template <int D, bool LN, bool QKV>
 __device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const float* __restrict__ ln,
                                         int8_t* __restrict__ q8, float* __restrict__ q_scale, const Geom& g,
-                                        const QkvDev& qa, int tile, int hk, int gi, int b, unsigned* gmax) {
+                                        const QkvDev& qa, int tile, int hk, int gi, int b, unsigned* gmax,
+                                        float* ginv) {
     constexpr int CH = D / 8;
     constexpr int TPI = 256 / CH;
     constexpr int NI = QTILE / TPI;
     const int tid = threadIdx.x, ch = tid % CH, slot = tid / CH;
     const bool f16 = g.flags & F_IN_F16;
+    const bool tail = (tile + 1) * QTILE > g.tokens;  // the tile holds padding rows (workgroup-uniform)
     {
         const int h = hk * g.group + gi;
         const long long bh = (long long)b * g.heads + h;
@@ -311,7 +313,7 @@ __device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const fl
                 qkv_row<D>(qv[i], qa, lq, tt, 0, ch);
             }
             if (LN) layernorm8<D>(qv[i], ln, ln + D, ch, g.ln_eps);
-            if ((LN || QKV) && tok >= g.tokens) {
+            if ((LN || QKV) && tail && tok >= g.tokens) {
 #pragma unroll
                 for (int e = 0; e < 8; e++) qv[i][e] = 0.f;  // padding rows stay zero
             }
@@ -323,11 +325,17 @@ __device__ __forceinline__ void tile_q8(const uint16_t* __restrict__ q, const fl
             if ((tid & 63) == 0) atomicMax(&gmax[(slot + i * TPI) / QGROUP], __float_as_uint(amax));
         }
         __syncthreads();
+        // Each 16-row group's 127 / amax (0 for an all-zero group), formed once
+        // a group and read back by the lanes of its rows.
+        if (tid < QTILE / QGROUP) {
+            const float amax = __uint_as_float(gmax[tid]);
+            ginv[tid] = amax > 0.f ? 127.0f / amax : 0.f;
+        }
+        __syncthreads();
 #pragma unroll
         for (int i = 0; i < NI; i++) {
             const int tl = slot + i * TPI;
-            const float amax = __uint_as_float(gmax[tl / QGROUP]);
-            const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+            const float inv = ginv[tl / QGROUP];
             const float* f = qv[i];
             uint2 w;
             w.x = s8x4(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
@@ -356,12 +364,13 @@ __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q,
                                                  float* __restrict__ part, int8_t* __restrict__ k8,
                                                  uint8_t* __restrict__ v8, Geom g, QkvDev qa) {
     __shared__ unsigned gmax[QTILE / QGROUP];
+    __shared__ float ginv[QTILE / QGROUP];
     __shared__ float red[8][4][D];
     constexpr int STATS = stat_roles<QKV>();
     const int roles = STATS + g.group, tile = (int)blockIdx.x / roles, role = (int)blockIdx.x % roles;
     const int hk = blockIdx.y, b = blockIdx.z;
     if (role >= STATS)
-        tile_q8<D, LN, QKV>(q, ln, q8, q_scale, g, qa, tile, hk, role - STATS, b, gmax);
+        tile_q8<D, LN, QKV>(q, ln, q8, q_scale, g, qa, tile, hk, role - STATS, b, gmax, ginv);
     else if (!QKV)
         tile_stats<D, LN, QKV, S_KV>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
     else if (role == 0)
