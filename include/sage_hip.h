@@ -223,12 +223,15 @@ sage_config sage_get_config(const sage_attention* s);        /* mod.rs:632-634 *
 void* sage_stream(const sage_attention* s);                  /* mod.rs:636-638 */
 
 /* attn_resources (mod.rs:640-646): VGPRs per lane and scratch (spill) bytes
- * of the attention kernel, plus its static LDS bytes. */
+ * of the attention kernel, plus its static LDS bytes. The kernel is the one
+ * the context's tile selects: the eight-wave layout for warps 8, else the
+ * four-wave kernel. */
 sage_status sage_attn_resources(const sage_attention* s, int32_t* regs, int32_t* spill, int32_t* lds);
 
 /* The same for each attention kernel the context can launch (extension: the
  * reference reports its dense kernel only): SAGE_KERNEL_DENSE, _CAUSAL (the
- * causal extension) or _MERGED (KV merging, sg_attn_merge). */
+ * causal extension) or _MERGED (KV merging, sg_attn_merge; always the
+ * four-wave kernel). */
 typedef enum sage_attn_kernel {
     SAGE_KERNEL_DENSE = 0,
     SAGE_KERNEL_CAUSAL = 1,
