@@ -42,8 +42,8 @@ def _spec(O, rng, D, heads, kv, batch, tokens, norm, rope, scaled, ld_pad=8, gri
     if rope is not None:
         s.rope = O.rope_table(rope, D, grid[0], grid[1], grid[2], 100.0)
         s.rope_layout = rope
-    y = rng.standard_normal((batch, tokens, s.ld)).astype(np.float32)
-    y[..., :s.width] += 0.5 * rng.standard_normal(s.width).astype(np.float32)  # per-channel offsets
+    y = rng.standard_normal((batch, tokens, s.ld), dtype=np.float32)
+    y[..., :s.width] += 0.5 * rng.standard_normal(s.width, dtype=np.float32)  # per-channel offsets
     return s, O.encode16(y, 0)
 
 
@@ -354,6 +354,31 @@ def test_fused_prepare_fuzz(oracle, torch_gpu, case):
     out = torch.empty((B, T, H, D), dtype=torch.bfloat16, device="cuda")
     qk_norm = S.QkNorm(torch.from_numpy(ln.copy()).to("cuda"), 1e-6) if c["sage_ln"] else None
     sa.forward_qkv(ws, inp, S.TensorMut(out), qn, rp, S.Options(causal=c["causal"], qk_norm=qk_norm))
+    torch.cuda.synchronize()
+    assert_prologue_equal(read_workspace(ws, p), want)
+    _, o_two = run(torch, p, q16, k16, v16, want_ws=False)
+    assert np.array_equal(from_device16(out), o_two)
+
+
+def test_fused_prepare_at_the_headline_shape(oracle, torch_gpu):
+    """C2's shape (B2 H32 N4096 D128) fed from the fused QKV projection with
+    every option of the bench's QKV workload (channel scales, bias, LayerNorm
+    QK-norm, VGGT RoPE over a 64-column grid): the workspace bit for bit
+    against the oracle, the output bit for bit against the two GPU steps."""
+    import spl_sage as S
+
+    torch = torch_gpu
+    B, H, T, D = 2, 32, 4096, 128
+    rng = np.random.default_rng(4242)
+    s, y = _spec(oracle, rng, D, H, 0, B, T, 1, 0, True, grid=(T // 64, 64, 0))
+    p = oracle.Problem(B, H, T, D, dtype=0)
+    q16, k16, v16 = oracle.qkv_prologue(s, y)
+    want = oracle.prologue(p, q16, k16, v16)
+    inp, qn, rp = _device(torch, s, y)
+    sa = S.SageAttention(None, D)
+    ws = sa.workspace(S.Shape(B, H, T))
+    out = torch.empty((B, T, H, D), dtype=torch.bfloat16, device="cuda")
+    sa.forward_qkv(ws, inp, S.TensorMut(out), qn, rp)
     torch.cuda.synchronize()
     assert_prologue_equal(read_workspace(ws, p), want)
     _, o_two = run(torch, p, q16, k16, v16, want_ws=False)
