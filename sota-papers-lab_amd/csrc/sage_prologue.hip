@@ -203,21 +203,26 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
             accumulate(tok, nullptr, fv);
         }
     } else if constexpr (QKV) {
-        // Rows of the fused projection carry their QKV-prologue arithmetic;
-        // two at a time keeps the registers of more waves (other waves hide
-        // the loads' latency).
-#pragma unroll 2
+        // K rows of the fused projection: every row's load issued first (one
+        // row at a time left each wave waiting on its load), then each row's
+        // QKV-prologue arithmetic, its stash and its sum.
+        static_assert(PART == S_K, "the fused statistics pass splits K and V");
+        uint4 kraw[NI];
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int tok = tile * QTILE + slot + i * TPI;
+            kraw[i] = load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, tok < g.tokens);
+        }
+#pragma unroll
         for (int i = 0; i < NI; i++) {
             const int tok = tile * QTILE + slot + i * TPI;
             const bool ok = tok < g.tokens;
             float fk[8], fv[8];
             QkvTok tt;
             qkv_tok<D>(tt, qa, g, 1, b, tok, ch);
-            unpack8(load16(k + b * g.k_sb + (long long)tok * g.k_st + hk * g.k_sh + ch * 8, ok), fk, false);
-            if (DO_V) unpack8(load16(v + b * g.v_sb + (long long)tok * g.v_st + hk * g.v_sh + ch * 8, ok), fv, false);
+            unpack8(kraw[i], fk, false);
             uint4 kbf;
             qkv_row<D>(fk, qa, lk, tt, 1, ch, &kbf);
-            if (DO_V) qkv_row<D>(fv, qa, lv, tt, 2, ch);
             if (g.merge == 1 && ok) *reinterpret_cast<uint4*>(k_stash(k8, v8, g, bhk, tok, ch, D)) = kbf;
             accumulate(tok, fk, fv);
         }
@@ -369,14 +374,16 @@ __global__ __launch_bounds__(256) void sage_prep(const uint16_t* __restrict__ q,
     constexpr int STATS = stat_roles<QKV>();
     const int roles = STATS + g.group, tile = (int)blockIdx.x / roles, role = (int)blockIdx.x % roles;
     const int hk = blockIdx.y, b = blockIdx.z;
-    if (role >= STATS)
+    if (role >= STATS) {
         tile_q8<D, LN, QKV>(q, ln, q8, q_scale, g, qa, tile, hk, role - STATS, b, gmax, ginv);
-    else if (!QKV)
+    } else if constexpr (!QKV) {
         tile_stats<D, LN, QKV, S_KV>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
-    else if (role == 0)
-        tile_stats<D, LN, QKV, S_K>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
-    else
-        tile_stats<D, LN, QKV, S_V>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
+    } else {
+        if (role == 0)
+            tile_stats<D, LN, QKV, S_K>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
+        else
+            tile_stats<D, LN, QKV, S_V>(k, v, ln, part, k8, v8, g, qa, tile, hk, b, red);
+    }
 }
 
 // sage_quant.cu:163-206 (sg_finalize): even and odd tiles folded separately,
