@@ -8,7 +8,9 @@ FP8 V) then attend (INT8 QK^T, online softmax, FP8 P.V) -- over one batch of
 synthetic inputs already resident in HBM. `value` is whole-step throughput in
 TOPS (4*B*H*N^2*D algorithmic ops per step, the reference's `flops`,
 mod.rs:905-910); `attention` reports the attention kernel alone, like the
-reference's attn_tops (tests.rs:968-971). One GPU only.
+reference's attn_tops (tests.rs:968-971). One GPU only. Before the W warm-up
+steps, untimed steps bring the warm-up to SETTLE steps in all, so that the
+timed steps run at the sustained shader clock (clock_settle_steps).
 
     python bench.py --vggt [--frames 200] [--merge 1|2|4] [--pv16] [--qk-norm]
 
@@ -34,7 +36,7 @@ sys.path.insert(0, str(ROOT / "sota-papers-lab_amd"))
 
 VENDOR_PEAK_TOPS = 5000.0   # MI355X dense INT8 (POPS) and FP8 (PFLOPS) MFMA, x1000
 VENDOR_HBM_GBS = 8000.0
-SETTLE = 100  # launches before the per-kernel timing (the clock ramps over ~60)
+SETTLE = 100  # untimed steps before the timed region (the clock ramps over ~60 launches)
 
 # Benchmark configurations C1-C5 as (B, H, HKV, N, D, dtype, causal, k_off_std, outlier_ch, outlier_scale, tok_frac, tok_scale)
 CONFIGS = {
@@ -552,6 +554,14 @@ def main() -> int:
                           "tops": round(ops / (ms * 1e-3) / 1e12, 2) if args.only == "attend" else None}), flush=True)
         return 0
 
+    # The shader clock ramps over the first ~60 attention launches of a
+    # process. Untimed steps before the W warm-up steps bring it to its
+    # sustained rate, so that the K timed steps measure that rate whatever W
+    # is: SETTLE steps before the timed region in all (reported as
+    # clock_settle_steps; none when W >= SETTLE).
+    pre = max(0, SETTLE - args.warmup)
+    for _ in range(pre):
+        step()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -562,13 +572,9 @@ def main() -> int:
     ms_per_step = max(ms_ev, wall_ms)
 
     # Per-kernel: the attention kernel alone and the prologue alone, the median
-    # of individually event-timed launches (tests.rs:733-748). The shader clock
-    # ramps over the first ~60 attention launches of a process, so the
-    # per-kernel figures are taken after at least SETTLE launches in all
-    # (warm-up and timed steps count; the rest are untimed attention launches).
-    settle = max(0, SETTLE - args.warmup - args.steps)
-    for _ in range(settle):
-        sa.attend(ws, ot)
+    # of individually event-timed launches (tests.rs:733-748), after the
+    # settled steps above.
+    settle = pre + args.warmup + args.steps
     attn_reps = max(args.steps, 20)
     attn_ms, attn_min, attn_mean = time_median(torch, stream, lambda: sa.attend(ws, ot), attn_reps)
     prep_ms, prep_min, prep_mean = time_median(torch, stream, lambda: sa.prepare(ws, qt, kt, vt, opts), attn_reps)
@@ -593,6 +599,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_settle_steps": pre,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

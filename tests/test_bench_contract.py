@@ -40,6 +40,8 @@ def test_json_line_carries_the_drivers_keys(torch_gpu):
         assert k in d, k
     assert d["metric"] == "attention TOPS @ B2 H32 N4096 D128; % of INT8/FP8 MFMA peak"
     assert d["unit"] == "TOPS" and d["n_gpus"] == 1 and d["steps"] == 5 and d["warmup"] == 3
+    # Untimed steps before the warm-up make 100 in all before the timed ones.
+    assert d["clock_settle_steps"] == 97
     assert d["higher_is_better"] is True and d["vs_baseline"] is None and d["value"] > 0
     assert d["config"]["workload"].startswith("C2 ") and "model" not in d["config"]
     roof = d["roofline"]
