@@ -217,14 +217,14 @@ __device__ __forceinline__ void tile_stats(const uint16_t* __restrict__ k, const
         for (int i = 0; i < NI; i++) {
             const int tok = tile * QTILE + slot + i * TPI;
             const bool ok = tok < g.tokens;
-            float fk[8], fv[8];
+            float fk[8];
             QkvTok tt;
             qkv_tok<D>(tt, qa, g, 1, b, tok, ch);
             unpack8(kraw[i], fk, false);
             uint4 kbf;
             qkv_row<D>(fk, qa, lk, tt, 1, ch, &kbf);
             if (g.merge == 1 && ok) *reinterpret_cast<uint4*>(k_stash(k8, v8, g, bhk, tok, ch, D)) = kbf;
-            accumulate(tok, fk, fv);
+            accumulate(tok, fk, nullptr);
         }
     } else {
         uint4 kraw[NI], vraw[NI];
