@@ -32,6 +32,9 @@ COMMON = [
     f"--offload-arch={ARCH}",
     "-Wall",
     "-Wno-unused-function",
+    # No packed fp32 (v_pk_fma_f32, v_pk_mul_f32, v_pk_add_f32) anywhere: on the
+    # MI355X machines this library is tested on, some of their forms have given
+    # wrong results now and then without an error.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 SCHED = ["-mllvm", "--amdgpu-sched-strategy=iterative-maxocc", "-mllvm", "--misched-postra-direction=bottomup"]
