@@ -95,7 +95,7 @@ static void qkv_row_f32(const oracle_qkv* a, const uint16_t* y, int b, int t, in
     if (part < 2 && a->norm) {
         const float* w = part == 0 ? a->q_w : a->k_w;
         const float* bb = part == 0 ? a->q_b : a->k_b;
-        float ls[16], l2[16], mean = 0.f;
+        float ls[16] = {0}, l2[16] = {0}, mean = 0.f;
         if (a->norm == ORACLE_NORM_LAYER) {
             for (int c = 0; c < CH; c++) {
                 float s = 0.f;
@@ -122,7 +122,7 @@ static void qkv_row_f32(const oracle_qkv* a, const uint16_t* y, int b, int t, in
             for (int c = 0; c < CH; c++) tt[c] = l2[c] + l2[c ^ o];
             memcpy(l2, tt, sizeof(float) * (size_t)CH);
         }
-        const float r = 1.0f / sqrtf(fmaf(l2[0], 1.0f / (float)D, a->eps));
+        const float r = oracle_rstd(fmaf(l2[0], 1.0f / (float)D, a->eps));
         for (int d = 0; d < D; d++)
             x[d] = fmaf((x[d] - mean) * r, w[d], a->norm == ORACLE_NORM_LAYER ? bb[d] : 0.0f);
     }

@@ -115,6 +115,10 @@ int oracle_s8(float x) {
 
 /* The reference's NVIDIA-fragment key permutation (reference.rs:74-76),
  * kept for its known-answer test (tests.rs:68-83) only. */
+/* IEEE single precision: sqrtf and the divide each round to nearest. Pinned
+ * by the closed forms of the LayerNorm tests (tests/test_oracle_qknorm.py). */
+float oracle_rstd(float v) { return 1.0f / sqrtf(v); }
+
 /* Pinned: numpy's float64 -> float16 conversion on random, tie, subnormal and
  * overflow values (tests/test_oracle_codecs.py). */
 double oracle_round_f16(double x) {
@@ -290,7 +294,7 @@ void oracle_layernorm(const float* x, float* y, int D, const float* w, const flo
         l2[c] = s2;
     }
     lane_butterfly(l2, CH);
-    const float rstd = 1.0f / sqrtf(fmaf(l2[0], 1.0f / (float)D, eps));
+    const float rstd = oracle_rstd(fmaf(l2[0], 1.0f / (float)D, eps));
     for (int i = 0; i < D; i++) y[i] = fmaf((x[i] - mean) * rstd, w[i], b[i]);
 }
 

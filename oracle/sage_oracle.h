@@ -111,6 +111,9 @@ int oracle_vpos_ref(int k);
  * the largest finite), returned as a double; the f16 accumulator of the
  * PvAccum::F16 emulation. */
 double oracle_round_f16(double x);
+/* The QK-norm's rstd: 1 / sqrt(v) with the square root and the divide each
+ * correctly rounded (1.0f / sqrtf(v) in IEEE arithmetic). */
+float oracle_rstd(float v);
 
 void oracle_decode16(const uint16_t* in, float* out, size_t n, int dtype);
 void oracle_encode16(const float* in, uint16_t* out, size_t n, int dtype);

@@ -87,7 +87,7 @@ __device__ __forceinline__ void layernorm8(float* x, const float* __restrict__ w
     }
 #pragma unroll
     for (int o = 1; o < CH; o <<= 1) s2 += __shfl_xor(s2, o, 64);
-    const float rstd = 1.0f / sqrtf(__builtin_fmaf(s2, 1.0f / D, eps));
+    const float rstd = rsqrt_rn2(__builtin_fmaf(s2, 1.0f / D, eps));
 #pragma unroll
     for (int e = 0; e < 8; e++) x[e] = __builtin_fmaf((x[e] - mean) * rstd, w[ch * 8 + e], bias[ch * 8 + e]);
 }
