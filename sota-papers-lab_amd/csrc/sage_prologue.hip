@@ -534,6 +534,18 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
     }
     float kv[NI][8];
     float amax = 0.f;
+    // The reference sums a dense key's (one) member from 0.0f first, so V's
+    // -0 becomes +0 before the mean is taken off: (v + 0) - mv. That equals
+    // v - mvz with mvz = -0 where mv is a zero of either sign (x - (-0) is
+    // x + 0) and mv elsewhere (where -0 - mv and +0 - mv agree), one operation
+    // fewer a value. It matters for V's E4M3 code (0x80 against 0x00) but not
+    // for K, whose |kv| and INT8 code drop the sign of a zero.
+    float mvz[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) mvz[e] = mv[e] == 0.0f ? -0.0f : mv[e];
+    // A block with no key past the sequence (all but a ragged last one) can
+    // run without the per-key guards (workgroup-uniform).
+    const bool full = (blk + 1) * KBLOCK <= g.tk;
     if (QKV && g.merge == 1) {
         // Rows of the fused projection: V first, then K, so that only one
         // part's channel constants (QkvLane) and statistics are live at a time.
@@ -557,7 +569,7 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
                 qkv_tok<D>(tt, qa, g, 2, b, blk * KBLOCK + kl, ch);
                 qkv_row<D>(fv, qa, lv, tt, 2, ch);
 #pragma unroll
-                for (int e = 0; e < 8; e++) vq[e] = ok ? ((fv[e] + 0.0f) - mv[e]) * iv[e] : 0.f;
+                for (int e = 0; e < 8; e++) vq[e] = ok ? (fv[e] - mvz[e]) * iv[e] : 0.f;
                 put_v(vt, ch, kl, vq);
             }
         }
@@ -580,8 +592,6 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
             if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                // The reference's (k + 0) - mean differs from k - mean only in
-                // the sign of a zero, which neither |kv| nor its INT8 code keeps.
                 kv[i][e] = ok ? fk[e] - mk[e] : 0.f;
                 amax = fmaxf(amax, fabsf(kv[i][e]));
             }
@@ -596,27 +606,30 @@ __global__ __launch_bounds__(256) void sage_quant_kv(const uint16_t* __restrict_
             vraw[i] = load16(v + b * g.v_sb + (long long)j * g.v_st + hk * g.v_sh + ch * 8, ok);
         }
         __syncthreads();
+        auto rows = [&](bool all) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < NI; i++) {
-            const int kl = slot + i * TPI;
-            const bool ok = blk * KBLOCK + kl < g.tk;
-            float fk[8], fv[8];
-            unpack8(kraw[i], fk, f16);
-            unpack8(vraw[i], fv, f16);
-            if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
-            float vq[8];
+            for (int i = 0; i < NI; i++) {
+                const int kl = slot + i * TPI;
+                const bool ok = all || blk * KBLOCK + kl < g.tk;
+                float fk[8], fv[8];
+                unpack8(kraw[i], fk, f16);
+                unpack8(vraw[i], fv, f16);
+                if (LN) layernorm8<D>(fk, ln + 2 * D, ln + 3 * D, ch, g.ln_eps);
+                float vq[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                // The reference sums the (one) member from 0.0f first, so -0
-                // becomes +0: that matters for V's E4M3 code (0x80 against
-                // 0x00) but not for K, whose |kv| and INT8 code drop the sign
-                // of a zero.
-                kv[i][e] = ok ? fk[e] - mk[e] : 0.f;
-                amax = fmaxf(amax, fabsf(kv[i][e]));
-                vq[e] = ok ? ((fv[e] + 0.0f) - mv[e]) * iv[e] : 0.f;
+                for (int e = 0; e < 8; e++) {
+                    kv[i][e] = ok ? fk[e] - mk[e] : 0.f;
+                    amax = fmaxf(amax, fabsf(kv[i][e]));
+                    vq[e] = ok ? (fv[e] - mvz[e]) * iv[e] : 0.f;
+                }
+                put_v(vt, ch, kl, vq);
             }
-            put_v(vt, ch, kl, vq);
-        }
+        };
+        // (The normed instantiation keeps one copy: two would cost it a wave.)
+        if (!LN && full)
+            rows(true);
+        else
+            rows(false);
     } else {
         __syncthreads();
         const int cells = g.merge * g.merge;  // uniform bound of the member loop

@@ -189,6 +189,38 @@ def test_constant_channels_come_out_exactly(oracle, torch_gpu):
     assert (o[..., 5] == c[0]).all() and (o[..., 77] == c[1]).all()
 
 
+@pytest.mark.parametrize("smooth_v", [True, False])
+@pytest.mark.parametrize("d", [64, 128])
+def test_v_negative_zeros(oracle, torch_gpu, smooth_v, d):
+    """V's -0 (bf16 0x8000) takes E4M3 code 0x00 wherever its channel's mean is
+    a zero, as the reference's (v + 0) - mean gives (sage_quant.cu:286-299, a
+    dense key summed from 0.0f), and the code of -mean elsewhere; the K and V
+    codes equal the oracle's bit for bit. Channels 0-15 hold +1 and -1 in equal
+    numbers (every partial sum exact, so the mean is exactly +0) with -0 at
+    every fifth token; the other channels are random with -0 at every seventh.
+    Without V smoothing every mean is 0. A ragged N (300) puts a padded last
+    key block beside full ones."""
+    p = oracle.Problem(1, 2, 300, d, smooth_v=smooth_v)
+    q, k, v = oracle.generate(p, oracle.GenSpec(k_off_std=2.0, seed=41))
+    one, neg_one, neg_zero = (int(x) for x in oracle.encode16(np.array([1.0, -1.0, -0.0], np.float32), 0))
+    t = np.arange(p.tokens)
+    sign = np.where((t // 5) % 2 == 0, one, neg_one)  # equal counts of +1 and -1 outside the -0 tokens
+    sign[t % 5 == 4] = neg_zero
+    pairs = (t % 5 != 4).sum()
+    assert (sign == one).sum() == (sign == neg_one).sum() == pairs // 2
+    v[:, :, :, :16] = sign[None, :, None, None].astype(np.uint16)
+    v[:, t % 7 == 3, :, 16:] = neg_zero
+    pro, o = run(torch_gpu, p, q, k, v)
+    want = oracle.prologue(p, q, k, v)
+    assert_prologue_equal(pro, want)
+    if smooth_v:
+        assert np.all(want["stats"][:, :, 1, :16].view(np.uint32) == 0)  # the mean is exactly +0
+    codes = want["v8"][:, :, :p.tokens]
+    assert np.all(codes[:, :, t % 5 == 4, :16] == 0x00)
+    if not smooth_v:
+        assert np.all(codes[:, :, t % 7 == 3, 16:] == 0x00)
+
+
 @pytest.mark.parametrize("d", [64, 128])
 def test_reference_tiles_give_identical_outputs(oracle, torch_gpu, d):
     """Every tile the reference accepts (Tile::validate, mod.rs:158-167) runs; the
